@@ -1,0 +1,99 @@
+/* Extension ABI of libmatvec_hip.so: the whole decode token loop resident on one MI355X.
+ *
+ * The drop-in API (matvec_fpga.h) moves only the GEMVs to the GPU, one synchronous call each.  This API
+ * is what the reference's hosts would call to move the rest of forward() too (qwen.c:490-573,
+ * runq.c:477-615): the model file is uploaded once (weights repacked into the GEMV tiles, KV cache in HBM),
+ * and one decode step is a fixed sequence of kernels that reads its position and token from device memory,
+ * captured once as a hipGraph and replayed per token.  Both of the reference's formats are accepted:
+ * .qwb (Qwen2, qwen.c:195-271) and llama2.c v2 .bin (runq, runq.c:318-357).
+ *
+ * Numerics follow the reference: int8 group quantization of activations (qwen.c:354-364 or runq.c:244-270,
+ * bit-exact for the same input), exact int32 group sums, the per-group product ((float)ival * ws) * xs,
+ * RoPE tables computed on the host with the reference's own libm calls.  Sums over groups, RMSNorm and
+ * softmax reductions run in parallel trees, so layer outputs match the reference within fp32 rounding.
+ * Errors: -1 (or NULL) with a message on stderr, the reference's convention (matvec_fpga.h:15). */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct llm_model llm_model;
+
+typedef struct {
+    int kind;                  /* 0: .qwb Qwen2 (qwen.c), 1: llama2.c v2 .bin (runq.c) */
+    int dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size;
+    int n_logits;              /* head_k (qwen.c:39) or vocab_size (runq) */
+    int ctx;                   /* KV cache positions: min(ctx, max_seq_len) (qwen.c:325) or seq_len (runq) */
+    int group_size;
+    float rope_theta, rms_eps;
+    double gemv_bytes_per_token; /* algorithmic GEMV bytes of one decode step: weights, scales, activations, outputs */
+    double weight_bytes;       /* resident tiled weight bytes in HBM */
+} llm_info;
+
+typedef struct {
+    int n_prompt, n_generated, n_forward;
+    double prompt_ms, decode_ms; /* decode: forwards after the prompt's last one, qwen.c:682, 709-711 */
+} llm_timing;
+
+/* build_transformer (qwen.c:320-330, runq.c:359-367): open, validate and upload a model.  ctx caps the
+ * KV cache for .qwb files (qwen's -c); .bin files always get seq_len positions.  NULL on failure. */
+llm_model *llm_open(const char *path, int ctx);
+int llm_get_info(const llm_model *m, llm_info *info);
+/* head_ids of a .qwb (qwen.c:57); NULL for .bin, whose logits are indexed by token id */
+const int32_t *llm_head_ids(const llm_model *m);
+
+/* forward (qwen.c:490-573, runq.c:477-615): one position; the logits of the head rows go to `logits`
+ * (n_logits floats, host memory) when it is not NULL.  Eager launches, synchronous. */
+int llm_forward(llm_model *m, int token, int pos, float *logits);
+
+/* generate with greedy sampling (qwen.c:669-712 at -t 0; runq.c:982-1036 at -t 0), the whole loop on the
+ * device: prompt forcing, argmax over the head rows, head_ids mapping, one hipGraph replay per position.
+ * Stop rules follow the model kind: .qwb stops at <|im_end|> 151645 / <|endoftext|> 151643, after
+ * max_new tokens or at a full context; .bin stops at BOS (1) or when max_new + n_prompt - 1 positions...
+ * (runq's steps clamp, runq.c:1200) are done.  Generated ids go to out (room for max_new).  When `logits`
+ * is not NULL, every position's head logits are appended to it (the --logits dump, qwen.c:676), so it needs
+ * room for (n_prompt + max_new) * n_logits floats.  Returns the number of generated ids, or -1. */
+int llm_generate(llm_model *m, const int *prompt, int n_prompt, int max_new, int *out, float *logits,
+                 llm_timing *timing);
+
+/* Decode throughput: replays the captured step graph `steps` times from the current position (after a
+ * prompt was forced by llm_generate or llm_forward) with no host round trips, and returns the elapsed time
+ * of exactly those replays in *ms (HIP events on the library's stream). */
+int llm_decode_replay(llm_model *m, int steps, double *ms);
+
+/* Per-kernel timing of decode steps: runs `steps` steps with HIP events around every launch (on the
+ * library's stream), and fills one record per kernel kind with its launch count, total device time and
+ * algorithmic bytes per launch.  Returns the number of records written (at most max_stats), or -1. */
+typedef struct {
+    char name[40];
+    int launches;
+    double total_ms;
+    double bytes_per_launch; /* algorithmic HBM bytes of one launch (weights + scales + activations + outputs) */
+} llm_kernel_stat;
+int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int max_stats);
+
+/* Batched prompt processing (prefill): positions 0..n-1 in one pass, int8 MFMA GEMMs for the layer
+ * matrices and causal attention; fills the KV cache like n forward() calls would and leaves the logits of
+ * the last position in `logits` (n_logits floats, may be NULL).  .qwb models only.  Returns 0 or -1. */
+int llm_prefill(llm_model *m, const int *ids, int n, float *logits);
+
+void llm_close(llm_model *m);
+
+/* ---- test hooks: no counterpart in the reference; they expose single device stages so the tests can
+ * hold each one against the oracle (like the reference's FPGA_CHECK side-by-side check, qwen.c:464-472) --- */
+
+/* activation quantization on the device: flavor 0 = qwen.c:354-364 (group 32), 1 = runq.c:244-270 (gs) */
+int mvh_quantize(const float *x, int n, int flavor, int gs, int8_t *q, float *s);
+/* exact int32 group sums of a matrix in the reference layout (qwen planes: bits 4 or 8, group 32; or runq
+ * int8 with group gs when bits == 0), computed by the GEMV kernels' own dot-product code: ival[d][n/gs] */
+int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, int bits, int gs, int32_t *ival);
+/* device state after the last llm_forward/llm_generate step: 0 = residual stream x (dim floats, after the
+ * final rmsnorm like qwen.c:569), 1 = key cache of layer `layer` (ctx * kv_dim), 2 = value cache */
+int llm_read_state(llm_model *m, int which, int layer, float *dst, size_t count);
+
+#ifdef __cplusplus
+}
+#endif

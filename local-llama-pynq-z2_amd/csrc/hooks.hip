@@ -1,0 +1,87 @@
+// Test hooks of include/llm_hip.h: single device stages on caller data, for the parity tests.
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/llm_hip.h"
+#include "host_common.h"
+
+namespace {
+int hook_device(const char *who) {
+    const int dev = hip_device_from_env(who);
+    if (dev < 0) return -1;
+    HIP_OR_FAIL(who, hipSetDevice(dev));
+    return 0;
+}
+} // namespace
+
+extern "C" int mvh_quantize(const float *x, int n, int flavor, int gs, int8_t *q, float *s) {
+    if (!x || !q || !s || n <= 0 || (gs != 32 && gs != 64) || n % gs || (flavor != QF_QWEN && flavor != QF_RUNQ) ||
+        (flavor == QF_QWEN && gs != 32) || n > 8192) {
+        fprintf(stderr, "mvh_quantize: bad arguments (n=%d gs=%d flavor=%d)\n", n, gs, flavor);
+        return -1;
+    }
+    if (hook_device("mvh_quantize")) return -1;
+    float *dx = nullptr, *ds = nullptr;
+    int8_t *dq = nullptr;
+    int rc = -1;
+    if (hipMalloc(&dx, (size_t)n * 4) == hipSuccess && hipMalloc(&dq, (size_t)n) == hipSuccess &&
+        hipMalloc(&ds, (size_t)n / gs * 4) == hipSuccess &&
+        hipMemcpy(dx, x, (size_t)n * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        launch_quantize_test(dx, n, flavor, gs, dq, ds, 0) == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+        hipMemcpy(q, dq, (size_t)n, hipMemcpyDeviceToHost) == hipSuccess &&
+        hipMemcpy(s, ds, (size_t)n / gs * 4, hipMemcpyDeviceToHost) == hipSuccess)
+        rc = 0;
+    else
+        fprintf(stderr, "mvh_quantize: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    hipFree(dx);
+    hipFree(dq);
+    hipFree(ds);
+    return rc;
+}
+
+extern "C" int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, int bits, int gs, int32_t *ival) {
+    const int wbits = bits == 0 ? 8 : bits;
+    if (!w || !xq || !ival || n <= 0 || d <= 0 || (bits != 0 && bits != 4 && bits != 8) || (gs != 32 && gs != 64) ||
+        (bits != 0 && gs != 32) || n % gs) {
+        fprintf(stderr, "mvh_group_dots: bad arguments (n=%d d=%d bits=%d gs=%d)\n", n, d, bits, gs);
+        return -1;
+    }
+    if (hook_device("mvh_group_dots")) return -1;
+    const int ng = n / gs;
+    TiledMat T = tiled_describe(d, n, gs, wbits, 0, 16);
+    const size_t wbytes = (size_t)d * n * wbits / 8, sbytes = (size_t)d * ng * 2;
+    uint8_t *dw = nullptr, *dsc = nullptr, *dt = nullptr;
+    int8_t *dx = nullptr;
+    int32_t *di = nullptr;
+    int *dmap = nullptr;
+    std::vector<int> map(d);
+    for (int i = 0; i < d; i++) map[i] = i;
+    int rc = -1;
+    if (hipMalloc(&dw, wbytes) == hipSuccess && hipMalloc(&dsc, sbytes) == hipSuccess &&
+        hipMalloc(&dt, T.bytes) == hipSuccess && hipMalloc(&dx, (size_t)n) == hipSuccess &&
+        hipMalloc(&di, (size_t)d * ng * 4) == hipSuccess && hipMalloc(&dmap, (size_t)d * 4) == hipSuccess &&
+        hipMemcpy(dw, w, wbytes, hipMemcpyHostToDevice) == hipSuccess && hipMemset(dsc, 0, sbytes) == hipSuccess &&
+        hipMemcpy(dx, xq, (size_t)n, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dmap, map.data(), (size_t)d * 4, hipMemcpyHostToDevice) == hipSuccess) {
+        T.data = dt;
+        RepackArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.T = T;
+        ra.w[0] = dw;
+        ra.s[0] = dsc;
+        ra.rowmap = dmap;
+        if (launch_repack(ra, 0) == hipSuccess && launch_group_dots_test(T, dx, di, 0) == hipSuccess &&
+            hipDeviceSynchronize() == hipSuccess &&
+            hipMemcpy(ival, di, (size_t)d * ng * 4, hipMemcpyDeviceToHost) == hipSuccess)
+            rc = 0;
+    }
+    if (rc) fprintf(stderr, "mvh_group_dots: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    hipFree(dw);
+    hipFree(dsc);
+    hipFree(dt);
+    hipFree(dx);
+    hipFree(di);
+    hipFree(dmap);
+    return rc;
+}

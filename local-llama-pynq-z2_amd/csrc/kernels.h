@@ -1,0 +1,101 @@
+// Kernel argument blocks and host-side launchers of libmatvec_hip.so (internal header).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tiled.h"
+
+// Per-step control block in device memory.  The step's kernels read the position and token from here,
+// so one captured graph serves every position.
+struct StepCtrl {
+    int pos;        // position of the current step
+    int token;      // input token of the current step
+    int next_token; // argmax of the current step, mapped through head_ids
+    int n_prompt;   // generate mode: positions < n_prompt take their token from the prompt
+    int mode;       // 0: pos/token set by the host; 1: the embed kernel advances pos and picks the token
+    int pad[3];
+};
+
+// Prologues: how the int8 activation vector reaches LDS.
+enum { PRO_XQ = 0, PRO_NORM = 1, PRO_ATTN = 2 };
+// Epilogues: what happens to the finished rows.
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_ARGMAX = 4 };
+// RoPE pairing of the fused QKV matrix.
+enum { ROPE_NEOX = 0, ROPE_INTERLEAVED = 1 };
+
+struct GemvArgs {
+    TiledMat W;
+    int kw, nb;             // waves per row-block, row-blocks per block iteration
+    int qflavor;            // activation quantization flavour (QF_QWEN / QF_RUNQ)
+    const StepCtrl *ctrl;
+    // PRO_XQ
+    const int8_t *xq;
+    const float *xs;
+    // PRO_NORM: x (n floats) -> rmsnorm(norm_w, eps) -> quantize
+    const float *x;
+    const float *norm_w;
+    float eps;
+    // PRO_ATTN: combine split attention partials -> quantize
+    const float *att_ml;    // [n_heads][splits][2] (max score, sum of exp)
+    const float *att_acc;   // [n_heads][splits][hs]
+    int n_heads, head_size, att_splits, att_chunk;
+    // EPI_STORE / EPI_RESID / EPI_ARGMAX: out[row] (= or +=)
+    float *out;
+    // EPI_ARGMAX
+    float *logits_hist;     // optional [ctx][rows]
+    float *part_val;
+    int *part_idx;
+    // EPI_QKV
+    const float *bias;      // [dim + 2*kv_dim] or NULL
+    float *q, *kc, *vc;     // q [dim]; layer bases of the caches [ctx][kv_dim]
+    const float *rope_cos, *rope_sin; // [ctx][head_size/2]
+    int dim, kv_dim, rope_kind;
+    // EPI_SWIGLU
+    int8_t *hq;
+    float *hs;
+    float *hf;              // optional fp32 h
+};
+
+struct AttnArgs {
+    const float *q;         // [n_heads * hs]
+    const float *kc, *vc;   // layer bases [ctx][kv_dim]
+    float *ml, *acc;        // partials, see GemvArgs
+    int n_heads, n_kv, hs, kv_dim, chunk, splits;
+    const StepCtrl *ctrl;
+};
+
+struct EmbedArgs {
+    const int8_t *emb_q;    // [vocab][dim]
+    const void *emb_s;      // [vocab][dim/gs] fp16 or fp32
+    int sf32, dim, gs;
+    float *x;
+    StepCtrl *ctrl;
+    const int *prompt;      // generate mode
+    int *tokens;            // [ctx] input token of every position
+};
+
+struct ArgmaxArgs {
+    const float *pv;
+    const int *pi;
+    int np;
+    const int *head_ids;    // NULL: identity
+    StepCtrl *ctrl;
+    int *gen;               // [ctx] argmax result of every position
+};
+
+struct RepackArgs {
+    TiledMat T;             // output (T.data writable)
+    const uint8_t *w[4];    // raw weight planes, row-major (reference layout)
+    const uint8_t *s[4];    // raw scale planes
+    const int *rowmap;      // logical row -> (source << 28) | source row
+};
+
+// host launchers (kernels.hip); each returns the launch error
+hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &a, int grid, hipStream_t st);
+size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads);
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+hipError_t launch_embed(const EmbedArgs &a, hipStream_t st);
+hipError_t launch_argmax(const ArgmaxArgs &a, hipStream_t st);
+hipError_t launch_repack(const RepackArgs &a, hipStream_t st);
+hipError_t launch_quantize_test(const float *x, int n, int flavor, int gs, int8_t *q, float *s, hipStream_t st);
+hipError_t launch_group_dots_test(const TiledMat &T, const int8_t *xq, int32_t *ival, hipStream_t st);

@@ -1,0 +1,577 @@
+// Kernels of libmatvec_hip.so for gfx950: tiled int4/int8 GEMV with fused prologues and epilogues,
+// decode attention, embedding lookup, argmax reduction and the weight repack.
+//
+// Reference roles: the GEMV is hls4/matvec4.cpp / hls/matvec.cpp (math in hls4/matvec4.h:1-4 and
+// hls/matvec.h:1-4, CPU form qwen.c:407-457 and runq.c:429-458); the prologues and epilogues are the
+// element-wise steps of forward() around each matmul (qwen.c:515-565, runq.c:497-605); attention is
+// qwen.c:526-546 / runq.c:530-568; argmax is qwen.c:591-598 with the head_ids map of qwen.c:683.
+#include "device.h"
+#include "kernels.h"
+
+#include <math.h>
+
+// ------------------------------------------------------------------------------------------------------
+// exact int32 group sums
+
+// int4 segment (16 B, repacked so dword j carries elements 4j..4j+3 low and 16+4j..16+4j+3 high) against
+// 32 int8 activations.  Each nibble is moved to the top of its byte, which reads it as 16 * (signed value)
+// with no sign extension; the sum is then exactly 16 * ival and one arithmetic shift recovers ival.
+__device__ __forceinline__ int dot_q4(const uint4 w, const uint32_t *x) {
+    int acc = 0;
+    acc = __builtin_amdgcn_sdot4((int)((w.x << 4) & 0xF0F0F0F0u), (int)x[0], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)(w.x & 0xF0F0F0F0u), (int)x[4], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)((w.y << 4) & 0xF0F0F0F0u), (int)x[1], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)(w.y & 0xF0F0F0F0u), (int)x[5], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)((w.z << 4) & 0xF0F0F0F0u), (int)x[2], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)(w.z & 0xF0F0F0F0u), (int)x[6], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)((w.w << 4) & 0xF0F0F0F0u), (int)x[3], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)(w.w & 0xF0F0F0F0u), (int)x[7], acc, false);
+    return acc >> 4;
+}
+
+// int8 segment of 16 bytes (piece) against 16 int8 activations
+__device__ __forceinline__ int dot_q8_piece(const uint4 w, const uint32_t *x, int acc) {
+    acc = __builtin_amdgcn_sdot4((int)w.x, (int)x[0], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)x[1], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)x[2], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)x[3], acc, false);
+    return acc;
+}
+
+template <int WB, int GSZ>
+__device__ __forceinline__ int seg_dot(const uint4 *wv, const uint32_t *x) {
+    if constexpr (WB == 4) {
+        return dot_q4(wv[0], x);
+    } else {
+        int acc = 0;
+#pragma unroll
+        for (int p = 0; p < GSZ / 16; p++) acc = dot_q8_piece(wv[p], x + 4 * p, acc);
+        return acc;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------
+// GEMV
+
+template <int WB, int GSZ, int SF32>
+struct Fmt {
+    static constexpr int SB = GSZ * WB / 8; // bytes per (row, group) segment
+    static constexpr int PIECES = SB / 16;
+    static constexpr int SCB = SF32 ? 4 : 2;
+};
+
+#define UNROLL 4
+
+__device__ __forceinline__ float rope_pair_out(float self, float partner, bool first, float c, float s) {
+    // qwen.c:483-485 / runq.c:516-519: first = a*c - b*s, second = b*c + a*s (a first, b second element)
+    if (first) {
+        float t1 = self * c, t2 = partner * s;
+        return t1 - t2;
+    }
+    float t1 = self * c, t2 = partner * s;
+    return t1 + t2;
+}
+
+template <int WB, int GSZ, int SF32, int PRO, int EPI>
+__global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
+    using F = Fmt<WB, GSZ, SF32>;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const TiledMat &W = a.W;
+    const int rb = W.rb, gpc = WAVE / rb, ngp = W.nchunks * gpc;
+    const int tid = threadIdx.x, nt = blockDim.x, wave = tid / WAVE, lane = tid & (WAVE - 1), nw = nt / WAVE;
+    const int n = W.n;
+    int8_t *sxq = (int8_t *)lds;                          // ngp * GSZ
+    float *sxs = (float *)(lds + (size_t)ngp * GSZ);      // ngp
+    float *sred = sxs + ngp;                              // nw * 64
+    float *srow = sred + nw * WAVE;                       // nb * rb
+    float *sv = srow + a.nb * rb;                         // prologue / epilogue floats
+    const int pos = (PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX) ? a.ctrl->pos : 0;
+
+    // ---- prologue: int8 activations and their scales into LDS
+    if constexpr (PRO == PRO_XQ) {
+        const uint32_t *src = (const uint32_t *)a.xq;
+        uint32_t *dst = (uint32_t *)sxq;
+        for (int i = tid; i < ngp * GSZ / 4; i += nt) dst[i] = i < n / 4 ? src[i] : 0u;
+        for (int i = tid; i < ngp; i += nt) sxs[i] = i < W.ng ? a.xs[i] : 0.0f;
+    } else {
+        if constexpr (PRO == PRO_NORM) {
+            // rmsnorm (qwen.c:337-344, runq.c:394-407): ss = sum x^2; ss /= n; ss += eps; ss = 1/sqrtf(ss)
+            float part = 0.0f;
+            for (int i = tid; i < n; i += nt) {
+                float v = a.x[i];
+                sv[i] = v;
+                part += v * v;
+            }
+            float ss = block_sum(part, sred);
+            ss /= (float)n;
+            ss += a.eps;
+            ss = 1.0f / sqrtf(ss);
+            for (int i = tid; i < n; i += nt) sv[i] = a.norm_w[i] * (ss * sv[i]);
+        } else { // PRO_ATTN: merge the split softmax partials of every head, then xb = acc / l
+            const int hs = a.head_size, S = a.att_splits;
+            const int active = min(S, pos / a.att_chunk + 1);
+            for (int i = tid; i < n; i += nt) {
+                const int h = i / hs, e = i - h * hs;
+                const float *ml = a.att_ml + (size_t)h * S * 2;
+                float m = ml[0];
+                for (int s = 1; s < active; s++) m = fmaxf(m, ml[2 * s]);
+                float l = 0.0f, v = 0.0f;
+                for (int s = 0; s < active; s++) {
+                    float f = expf(ml[2 * s] - m);
+                    l += ml[2 * s + 1] * f;
+                    v += a.att_acc[((size_t)h * S + s) * hs + e] * f;
+                }
+                sv[i] = v / l;
+            }
+        }
+        __syncthreads();
+        block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
+        for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
+        for (int i = W.ng + tid; i < ngp; i += nt) sxs[i] = 0.0f;
+    }
+    __syncthreads();
+
+    // ---- main loop over groups of nb row-blocks
+    const int my_nb = wave / a.kw, my_kw = wave - my_nb * a.kw;
+    const int rows_it = a.nb * rb;
+    const int n_it = (W.nblocks + a.nb - 1) / a.nb;
+    float best_v = -INFINITY;
+    int best_i = 0x7fffffff;
+    for (int it = blockIdx.x; it < n_it; it += gridDim.x) {
+        const int b = it * a.nb + my_nb;
+        float acc = 0.0f;
+        if (b < W.nblocks) {
+            const uint8_t *base = W.data + (size_t)b * W.nchunks * W.rec;
+            const int g_lane = lane / rb;
+            for (int c0 = my_kw; c0 < W.nchunks; c0 += a.kw * UNROLL) {
+                uint4 wv[UNROLL][F::PIECES];
+                uint32_t sr[UNROLL];
+#pragma unroll
+                for (int u = 0; u < UNROLL; u++) {
+                    const int c = c0 + u * a.kw;
+                    if (c < W.nchunks) {
+                        const uint8_t *rec = base + (size_t)c * W.rec;
+#pragma unroll
+                        for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
+                        if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
+                        else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < UNROLL; u++) {
+                    const int c = c0 + u * a.kw;
+                    if (c < W.nchunks) {
+                        const int g = c * gpc + g_lane;
+                        const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
+                        const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
+                        float p = (float)iv * sc; // qwen.c:452, runq.c:452: ((float)ival * ws) * xs
+                        p = p * sxs[g];
+                        acc = acc + p;
+                    }
+                }
+            }
+        }
+        acc = wave_sum_from(acc, rb); // lanes holding the same row
+        if (lane < rb) sred[wave * rb + lane] = acc;
+        __syncthreads();
+        if (tid < rows_it) {
+            const int nbi = tid / rb, r = tid - nbi * rb;
+            float v = 0.0f;
+            for (int k = 0; k < a.kw; k++) v += sred[(nbi * a.kw + k) * rb + r];
+            srow[tid] = v;
+        }
+        __syncthreads();
+
+        // ---- epilogue
+        const int R = it * rows_it + tid; // logical row of this thread
+        if constexpr (EPI == EPI_STORE) {
+            if (tid < rows_it && R < W.rows) a.out[R] = srow[tid];
+        } else if constexpr (EPI == EPI_RESID) {
+            if (tid < rows_it && R < W.rows) a.out[R] += srow[tid]; // qwen.c:551, 565
+        } else if constexpr (EPI == EPI_ARGMAX) {
+            if (tid < rows_it && R < W.rows) {
+                const float v = srow[tid];
+                a.out[R] = v;
+                if (a.logits_hist) a.logits_hist[(size_t)pos * W.rows + R] = v;
+                if (v > best_v) { best_v = v; best_i = R; } // rows grow with it: strict > keeps the first
+            }
+        } else if constexpr (EPI == EPI_QKV) {
+            if (tid < rows_it && R < W.rows) {
+                const int dim = a.dim, kvd = a.kv_dim, hs = a.head_size, half = hs / 2;
+                float v = srow[tid];
+                if (a.rope_kind == ROPE_NEOX) {
+                    // rows [0, dim + kv) hold q then k in blocks of 16: 8 first-half rows, then their 8 partners
+                    if (R < dim + kvd) {
+                        const int blk = R / 16, r = R & 15, per = half / 8;
+                        const int hh = blk / per, i0 = (blk - hh * per) * 8, i = i0 + (r & 7);
+                        const int e = hh * hs + (r < 8 ? i : half + i);
+                        const int ep = hh * hs + (r < 8 ? half + i : i);
+                        float self = v + a.bias[e], partner = srow[tid ^ 8] + a.bias[ep];
+                        const float c = a.rope_cos[(size_t)pos * half + i], s = a.rope_sin[(size_t)pos * half + i];
+                        float o = rope_pair_out(self, partner, r < 8, c, s);
+                        if (e < dim) a.q[e] = o;
+                        else a.kc[(size_t)pos * kvd + (e - dim)] = o;
+                    } else {
+                        const int e = R - dim - kvd;
+                        a.vc[(size_t)pos * kvd + e] = v + a.bias[dim + kvd + e];
+                    }
+                } else {
+                    // natural order q, k, v; pairs (2i, 2i+1) rotate (runq.c:506-521)
+                    if (R < dim + kvd) {
+                        const int e = R < dim ? R : R - dim;
+                        const int i = (e % hs) / 2;
+                        const float c = a.rope_cos[(size_t)pos * half + i], s = a.rope_sin[(size_t)pos * half + i];
+                        const bool first = (e & 1) == 0;
+                        const float partner = srow[tid ^ 1];
+                        // first: v0*fcr - v1*fci; second: v0*fci + v1*fcr (v0 first, v1 second)
+                        float o;
+                        if (first) { float t1 = v * c, t2 = partner * s; o = t1 - t2; }
+                        else { float t1 = partner * s, t2 = v * c; o = t1 + t2; }
+                        if (R < dim) a.q[e] = o;
+                        else a.kc[(size_t)pos * kvd + e] = o;
+                    } else {
+                        a.vc[(size_t)pos * kvd + (R - dim - kvd)] = v;
+                    }
+                }
+            }
+        } else if constexpr (EPI == EPI_SWIGLU) {
+            // each row-block holds rb/2 gate rows then the rb/2 matching up rows (qwen.c:556-562)
+            const int hb = rb / 2, per_it = a.nb * hb;
+            if (tid < rows_it) {
+                const int nbi = tid / rb, r = tid - nbi * rb;
+                if (r < hb) {
+                    float g = srow[tid], u = srow[tid + hb];
+                    float sig = 1.0f / (1.0f + expf(-g));
+                    g = g * sig;
+                    sv[nbi * hb + r] = g * u;
+                }
+            }
+            __syncthreads();
+            const int j0 = it * per_it;
+            if (j0 < a.dim) { // a.dim holds the hidden size here
+                const int cnt = min(per_it, a.dim - j0);
+                if (a.hf)
+                    for (int i = tid; i < cnt; i += nt) a.hf[j0 + i] = sv[i];
+                block_quantize(sv, cnt, W.gs, a.qflavor, a.hq + j0, a.hs + j0 / W.gs);
+            }
+        }
+        __syncthreads();
+    }
+    if constexpr (EPI == EPI_ARGMAX) {
+        // block argmax: larger value wins, equal values keep the lower row (first strict maximum)
+        float v = best_v;
+        int i = best_i;
+        for (int off = 1; off < WAVE; off <<= 1) {
+            float ov = __shfl_xor(v, off);
+            int oi = __shfl_xor(i, off);
+            if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+        }
+        int *si = (int *)(sred + nw);
+        if (lane == 0) { sred[wave] = v; si[wave] = i; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int k = 1; k < nw; k++)
+                if (sred[k] > v || (sred[k] == v && si[k] < i)) { v = sred[k]; i = si[k]; }
+            a.part_val[blockIdx.x] = v;
+            a.part_idx[blockIdx.x] = i;
+        }
+    }
+}
+
+size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
+    const TiledMat &W = a.W;
+    const int ngp = W.nchunks * (WAVE / W.rb);
+    size_t b = (size_t)ngp * W.gs + (size_t)ngp * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
+    size_t extra = 0;
+    if (pro != PRO_XQ) extra = (size_t)W.n * 4;
+    if (epi == EPI_SWIGLU) extra = extra > (size_t)a.nb * W.rb * 2 ? extra : (size_t)a.nb * W.rb * 2;
+    return b + extra + 16;
+}
+
+template <int WB, int GSZ, int SF32, int PRO, int EPI>
+static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
+    const int threads = a.kw * a.nb * WAVE;
+    const size_t lds = gemv_lds_bytes(a, PRO, EPI, threads);
+    hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI>), dim3(grid), dim3(threads), lds, st, a);
+    return hipGetLastError();
+}
+
+template <int WB, int GSZ, int SF32>
+static hipError_t launch_fmt(int pro, int epi, const GemvArgs &a, int grid, hipStream_t st) {
+#define CASE(P, E) if (pro == P && epi == E) return launch_one<WB, GSZ, SF32, P, E>(a, grid, st)
+    CASE(PRO_XQ, EPI_STORE);
+    CASE(PRO_XQ, EPI_RESID);
+    CASE(PRO_NORM, EPI_QKV);
+    CASE(PRO_ATTN, EPI_RESID);
+    CASE(PRO_NORM, EPI_SWIGLU);
+    CASE(PRO_NORM, EPI_ARGMAX);
+#undef CASE
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &a, int grid, hipStream_t st) {
+    if (wbits == 4 && gs == 32 && !sf32) return launch_fmt<4, 32, 0>(pro, epi, a, grid, st);
+    if (wbits == 8 && gs == 32 && !sf32) return launch_fmt<8, 32, 0>(pro, epi, a, grid, st);
+    if (wbits == 8 && gs == 32 && sf32) return launch_fmt<8, 32, 1>(pro, epi, a, grid, st);
+    if (wbits == 8 && gs == 64 && sf32) return launch_fmt<8, 64, 1>(pro, epi, a, grid, st);
+    return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------------------------------------------
+// decode attention (qwen.c:526-546, runq.c:530-568), split over positions: block (kv head, split) covers
+// `chunk` positions for the kv_mul query heads that share the kv head; it writes the split's max score,
+// sum of exponentials and exp-weighted value sum, which the o-projection's prologue merges.
+
+__global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    const int pos = a.ctrl->pos;
+    const int kvh = blockIdx.x / a.splits, s = blockIdx.x - kvh * a.splits;
+    const int t0 = s * a.chunk;
+    if (t0 > pos) return;
+    const int T = min(a.chunk, pos + 1 - t0);
+    const int hs = a.hs, kv_mul = a.n_heads / a.n_kv, tid = threadIdx.x, nt = blockDim.x;
+    const int wave = tid / WAVE, lane = tid & (WAVE - 1), nw = nt / WAVE;
+    float *sq = sm;                       // kv_mul * hs
+    float *sc = sq + kv_mul * hs;         // kv_mul * chunk
+    float *sp = sc + kv_mul * a.chunk;    // partial sums: slices * kv_mul * hs
+    const float *K = a.kc + (size_t)t0 * a.kv_dim + (size_t)kvh * hs;
+    const float *V = a.vc + (size_t)t0 * a.kv_dim + (size_t)kvh * hs;
+    for (int i = tid; i < kv_mul * hs; i += nt) sq[i] = a.q[(size_t)kvh * kv_mul * hs + i];
+    __syncthreads();
+    // scores: score = (q . k) / sqrtf(hs)
+    const float rs = sqrtf((float)hs);
+    for (int t = tid; t < T; t += nt) {
+        const float *k = K + (size_t)t * a.kv_dim;
+        for (int j0 = 0; j0 < kv_mul; j0 += 8) {
+            float sacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int i = 0; i < hs; i += 4) {
+                const float4 kv4 = *(const float4 *)(k + i);
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) {
+                    if (j0 + jj < kv_mul) { // score += q[i] * k[i] in order (qwen.c:535)
+                        const float *qq = sq + (j0 + jj) * hs + i;
+                        sacc[jj] += qq[0] * kv4.x;
+                        sacc[jj] += qq[1] * kv4.y;
+                        sacc[jj] += qq[2] * kv4.z;
+                        sacc[jj] += qq[3] * kv4.w;
+                    }
+                }
+            }
+            for (int jj = 0; jj < 8 && j0 + jj < kv_mul; jj++) sc[(j0 + jj) * a.chunk + t] = sacc[jj] / rs;
+        }
+    }
+    __syncthreads();
+    // softmax statistics per head: one wave per head
+    for (int j = wave; j < kv_mul; j += nw) {
+        float m = -INFINITY;
+        for (int t = lane; t < T; t += WAVE) m = fmaxf(m, sc[j * a.chunk + t]);
+        m = group_max(m, WAVE);
+        float l = 0.0f;
+        for (int t = lane; t < T; t += WAVE) {
+            float e = expf(sc[j * a.chunk + t] - m);
+            sc[j * a.chunk + t] = e;
+            l += e;
+        }
+        l = wave_sum_from(l, 1);
+        if (lane == 0) {
+            float *ml = a.ml + ((size_t)(kvh * kv_mul + j) * a.splits + s) * 2;
+            ml[0] = m;
+            ml[1] = l;
+        }
+    }
+    __syncthreads();
+    // weighted values: thread (slice, e) sums positions t = slice, slice + slices, ...
+    const int slices = nt / hs;
+    const int sl = tid / hs, e = tid - sl * hs;
+    if (sl < slices) {
+        float acc[16];
+        for (int j = 0; j < 16; j++) acc[j] = 0.0f;
+        for (int t = sl; t < T; t += slices) {
+            const float v = V[(size_t)t * a.kv_dim + e];
+            for (int j = 0; j < kv_mul && j < 16; j++) acc[j] += sc[j * a.chunk + t] * v;
+        }
+        for (int j = 0; j < kv_mul && j < 16; j++) sp[((size_t)sl * kv_mul + j) * hs + e] = acc[j];
+    }
+    __syncthreads();
+    for (int i = tid; i < kv_mul * hs; i += nt) {
+        const int j = i / hs, ee = i - j * hs;
+        float v = 0.0f;
+        for (int k = 0; k < slices; k++) v += sp[((size_t)k * kv_mul + j) * hs + ee];
+        a.acc[((size_t)(kvh * kv_mul + j) * a.splits + s) * hs + ee] = v;
+    }
+}
+
+hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
+    const int kv_mul = a.n_heads / a.n_kv, threads = 256;
+    const int slices = threads / a.hs;
+    const size_t lds = ((size_t)kv_mul * a.hs + (size_t)kv_mul * a.chunk + (size_t)slices * kv_mul * a.hs) * 4;
+    hipLaunchKernelGGL(k_attention, dim3(a.n_kv * a.splits), dim3(threads), lds, st, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------------
+// embedding row (qwen.c:498-501, runq.c:490-492) and the step's position/token bookkeeping
+
+__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
+    __shared__ int tok_s;
+    if (threadIdx.x == 0) {
+        StepCtrl *c = a.ctrl;
+        int pos = c->pos, token = c->token;
+        if (c->mode == 1) {
+            pos = pos + 1;
+            token = pos < c->n_prompt ? a.prompt[pos] : c->next_token;
+            c->pos = pos;
+            c->token = token;
+        }
+        if (a.tokens) a.tokens[pos] = token;
+        tok_s = token;
+    }
+    __syncthreads();
+    const int token = tok_s, ngr = a.dim / a.gs;
+    const int8_t *er = a.emb_q + (size_t)token * a.dim;
+    for (int i = threadIdx.x; i < a.dim; i += blockDim.x) {
+        const int g = i / a.gs;
+        const float sc = a.sf32 ? ((const float *)a.emb_s)[(size_t)token * ngr + g]
+                                : f16_bits_to_f32(((const uint16_t *)a.emb_s)[(size_t)token * ngr + g]);
+        a.x[i] = (float)er[i] * sc;
+    }
+}
+
+hipError_t launch_embed(const EmbedArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// final argmax over the per-block partials (qwen.c:591-598) and the head_ids map (qwen.c:683)
+__global__ void __launch_bounds__(256) k_argmax(ArgmaxArgs a) {
+    __shared__ float sv[256 / WAVE];
+    __shared__ int si[256 / WAVE];
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    for (int k = threadIdx.x; k < a.np; k += blockDim.x) {
+        const float pv = a.pv[k];
+        const int pi = a.pi[k];
+        if (pv > v || (pv == v && pi < i)) { v = pv; i = pi; }
+    }
+    for (int off = 1; off < WAVE; off <<= 1) {
+        float ov = __shfl_xor(v, off);
+        int oi = __shfl_xor(i, off);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    if (lane == 0) { sv[wave] = v; si[wave] = i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < (int)(blockDim.x / WAVE); k++)
+            if (sv[k] > v || (sv[k] == v && si[k] < i)) { v = sv[k]; i = si[k]; }
+        if (i == 0x7fffffff) i = 0; // every logit NaN: the reference keeps row 0
+        const int next = a.head_ids ? a.head_ids[i] : i;
+        a.ctrl->next_token = next;
+        if (a.gen) a.gen[a.ctrl->pos] = next;
+    }
+}
+
+hipError_t launch_argmax(const ArgmaxArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------------
+// repack: reference row-major planes -> chunk records (layout in tiled.h).  One thread per (record, lane).
+
+__global__ void k_repack(RepackArgs a) {
+    const TiledMat &T = a.T;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nrec = (size_t)T.nblocks * T.nchunks;
+    if (gid >= nrec * WAVE) return;
+    const int lane = (int)(gid % WAVE);
+    const size_t recno = gid / WAVE;
+    const int b = (int)(recno / T.nchunks), c = (int)(recno - (size_t)b * T.nchunks);
+    const int rb = T.rb, row = b * rb + lane % rb, g = c * (WAVE / rb) + lane / rb;
+    const int sb = T.gs * T.wbits / 8, scb = T.sf32 ? 4 : 2;
+    uint8_t *rec = (uint8_t *)T.data + recno * T.rec;
+    uint8_t seg[64];
+    uint32_t sc = 0;
+    for (int i = 0; i < sb; i++) seg[i] = 0;
+    if (row < T.rows && g < T.ng) {
+        const int m = a.rowmap[row];
+        const int src = m >> 28, sr = m & 0x0fffffff;
+        const size_t rowbytes = (size_t)T.n * T.wbits / 8;
+        const uint8_t *w = a.w[src] + (size_t)sr * rowbytes + (size_t)g * sb;
+        if (T.wbits == 4) {
+            // element e of the group sits in byte e/2, low nibble for even e (qwen.c:45, 447)
+            for (int j = 0; j < 4; j++)
+                for (int k = 0; k < 4; k++) {
+                    const int e0 = 4 * j + k, e1 = 16 + 4 * j + k;
+                    const int n0 = (w[e0 >> 1] >> ((e0 & 1) * 4)) & 15, n1 = (w[e1 >> 1] >> ((e1 & 1) * 4)) & 15;
+                    seg[4 * j + k] = (uint8_t)(n0 | (n1 << 4));
+                }
+        } else {
+            for (int i = 0; i < sb; i++) seg[i] = w[i];
+        }
+        const uint8_t *s = a.s[src] + ((size_t)sr * T.ng + g) * scb;
+        sc = scb == 4 ? (uint32_t)s[0] | ((uint32_t)s[1] << 8) | ((uint32_t)s[2] << 16) | ((uint32_t)s[3] << 24)
+                      : (uint32_t)s[0] | ((uint32_t)s[1] << 8);
+    }
+    for (int p = 0; p < sb / 16; p++) {
+        uint4 v;
+        v.x = seg[16 * p + 0] | (seg[16 * p + 1] << 8) | (seg[16 * p + 2] << 16) | ((uint32_t)seg[16 * p + 3] << 24);
+        v.y = seg[16 * p + 4] | (seg[16 * p + 5] << 8) | (seg[16 * p + 6] << 16) | ((uint32_t)seg[16 * p + 7] << 24);
+        v.z = seg[16 * p + 8] | (seg[16 * p + 9] << 8) | (seg[16 * p + 10] << 16) | ((uint32_t)seg[16 * p + 11] << 24);
+        v.w = seg[16 * p + 12] | (seg[16 * p + 13] << 8) | (seg[16 * p + 14] << 16) | ((uint32_t)seg[16 * p + 15] << 24);
+        *(uint4 *)(rec + (size_t)p * 1024 + lane * 16) = v;
+    }
+    if (scb == 4) *(uint32_t *)(rec + (size_t)WAVE * sb + lane * 4) = sc;
+    else *(uint16_t *)(rec + (size_t)WAVE * sb + lane * 2) = (uint16_t)sc;
+}
+
+hipError_t launch_repack(const RepackArgs &a, hipStream_t st) {
+    const size_t threads = (size_t)a.T.nblocks * a.T.nchunks * WAVE;
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------------
+// test hooks
+
+__global__ void __launch_bounds__(256) k_quantize_test(const float *x, int n, int flavor, int gs, int8_t *q, float *s) {
+    extern __shared__ float xv[];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) xv[i] = x[i];
+    __syncthreads();
+    block_quantize(xv, n, gs, flavor, q, s);
+}
+
+hipError_t launch_quantize_test(const float *x, int n, int flavor, int gs, int8_t *q, float *s, hipStream_t st) {
+    hipLaunchKernelGGL(k_quantize_test, dim3(1), dim3(256), (size_t)n * 4, st, x, n, flavor, gs, q, s);
+    return hipGetLastError();
+}
+
+// per-(row, group) int32 sums through the GEMV's own seg_dot on tiled records
+template <int WB, int GSZ>
+__global__ void k_group_dots(TiledMat T, const int8_t *xq, int32_t *ival) {
+    using F = Fmt<WB, GSZ, 0>;
+    const size_t gid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nrec = (size_t)T.nblocks * T.nchunks;
+    if (gid >= nrec * WAVE) return;
+    const int lane = (int)(gid % WAVE);
+    const size_t recno = gid / WAVE;
+    const int b = (int)(recno / T.nchunks), c = (int)(recno - (size_t)b * T.nchunks);
+    const int row = b * T.rb + lane % T.rb, g = c * (WAVE / T.rb) + lane / T.rb;
+    if (row >= T.rows || g >= T.ng) return;
+    const uint8_t *rec = T.data + recno * T.rec;
+    uint4 wv[F::PIECES];
+    for (int p = 0; p < F::PIECES; p++) wv[p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
+    uint32_t xw[GSZ / 4];
+    for (int k = 0; k < GSZ / 4; k++) xw[k] = ((const uint32_t *)(xq + (size_t)g * GSZ))[k];
+    ival[(size_t)row * T.ng + g] = seg_dot<WB, GSZ>(wv, xw);
+}
+
+hipError_t launch_group_dots_test(const TiledMat &T, const int8_t *xq, int32_t *ival, hipStream_t st) {
+    const size_t threads = (size_t)T.nblocks * T.nchunks * WAVE;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (T.wbits == 4 && T.gs == 32) hipLaunchKernelGGL((k_group_dots<4, 32>), grid, dim3(256), 0, st, T, xq, ival);
+    else if (T.wbits == 8 && T.gs == 32) hipLaunchKernelGGL((k_group_dots<8, 32>), grid, dim3(256), 0, st, T, xq, ival);
+    else if (T.wbits == 8 && T.gs == 64) hipLaunchKernelGGL((k_group_dots<8, 64>), grid, dim3(256), 0, st, T, xq, ival);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}

@@ -1,0 +1,315 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each oracle function is held against (1) the committed golden vectors written by the reference's own
+compiled C (tests/golden/make_golden.py), (2) the reference functions themselves when oracle/_ref/ is
+built, and (3) closed forms chosen so that a plausible slip (wrong rounding mode, dropped term, swapped
+operand, wrong nibble) fails."""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+from helpers import GOLDEN, OracleModel, exact_terms, f16_scales, oracle, ptr, ref_lib, unpack_q4
+
+OPS = np.load(os.path.join(GOLDEN, "ops.npz"))
+
+
+def test_f16_every_pattern():
+    L = oracle()
+    bits = np.arange(65536, dtype=np.uint16)
+    mine = np.array([L.or_f16(int(b)) for b in bits], np.float32)
+    want = bits.view(np.float16).astype(np.float32)  # IEEE binary16 -> binary32 is exact
+    same = (mine == want) | (np.isnan(mine) & np.isnan(want))
+    assert same.all()
+    # the reference's own f16() on every exponent it accepts (golden)
+    got = np.array([L.or_f16(int(b)) for b in OPS["f16_bits"]], np.float32)
+    assert np.array_equal(got, OPS["f16_vals"])
+
+
+def test_f32_to_f16_round_trip():
+    L = oracle()
+    bits = np.arange(0, 65536, dtype=np.uint16)
+    finite = bits[((bits >> 10) & 31) != 31]
+    back = np.array([L.or_f32_to_f16(float(v)) for v in finite.view(np.float16).astype(np.float32)], np.uint16)
+    zero = (finite & 0x7FFF) == 0
+    assert np.array_equal(back[~zero], finite[~zero])
+    vals = np.random.default_rng(3).standard_normal(2000).astype(np.float32) * 0.01
+    want = vals.astype(np.float16).view(np.uint16)  # numpy rounds to nearest even
+    got = np.array([L.or_f32_to_f16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, want)
+
+
+def quantize_qwen(x):
+    q, s = np.empty(x.size, np.int8), np.empty(x.size // 32, np.float32)
+    oracle().or_quantize_qwen(ptr(q), ptr(s), ptr(x), x.size)
+    return q, s
+
+
+def quantize_runq(x, gs):
+    q, s = np.empty(x.size, np.int8), np.empty(x.size // gs, np.float32)
+    oracle().or_quantize_runq(ptr(q), ptr(s), ptr(x), x.size, gs)
+    return q, s
+
+
+def test_quantize_qwen_golden():
+    q, s = quantize_qwen(OPS["q_x"])
+    assert np.array_equal(q, OPS["qwen_q"]) and np.array_equal(s.view(np.uint32), OPS["qwen_s"].view(np.uint32))
+
+
+@pytest.mark.parametrize("gs", [32, 64])
+def test_quantize_runq_golden(gs):
+    q, s = quantize_runq(OPS["q_x"], gs)
+    assert np.array_equal(q, OPS[f"runq{gs}_q"])
+    assert np.array_equal(s.view(np.uint32), OPS[f"runq{gs}_s"].view(np.uint32))
+
+
+def test_quantize_closed_forms():
+    # a group whose max is 127: scale 1 exactly, so q = round-half-away-from-zero of x itself
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:] = np.arange(31, dtype=np.float32) - 15.5
+    q, s = quantize_qwen(x)
+    assert s[0] == np.float32(127.0) * np.float32(1.0 / 127.0)
+    halves = x[1:] / (s[0])
+    want = np.sign(halves) * np.floor(np.abs(halves) + 0.5)
+    assert np.array_equal(q[1:], want.astype(np.int8))
+    assert q[0] == 127
+    q, s = quantize_qwen(np.zeros(32, np.float32))
+    assert s[0] == 0 and not q.any()
+    qr, sr = quantize_runq(np.zeros(64, np.float32), 64)
+    assert sr[0] == 0 and not qr.any()
+    # the extreme of every group maps to +-127 in both flavours
+    x = np.random.default_rng(1).standard_normal(32 * 50).astype(np.float32)
+    for q, g in ((quantize_qwen(x)[0], 32), (quantize_runq(x, 32)[0], 32)):
+        qa = np.abs(q.reshape(-1, g).astype(int)).max(1)
+        assert (qa == 127).all()
+
+
+def test_quantize_against_reference_live():
+    R, Q = ref_lib("runq"), ref_lib("qwen")
+    if R is None or Q is None:
+        pytest.skip("oracle/_ref not built")
+    x = (np.random.default_rng(7).standard_normal(64 * 300) * np.logspace(-3, 3, 64 * 300)).astype(np.float32)
+    rq, rs = np.empty(x.size, np.int8), np.empty(x.size // 32, np.float32)
+    Q.refq_quantize(ptr(rq), ptr(rs), ptr(x), C.c_int(x.size))
+    q, s = quantize_qwen(x)
+    assert np.array_equal(q, rq) and np.array_equal(s, rs)
+    for gs in (32, 64):
+        rq, rs = np.empty(x.size, np.int8), np.empty(x.size // gs, np.float32)
+        R.refr_quantize(ptr(rq), ptr(rs), ptr(x), C.c_int(x.size), C.c_int(gs))
+        q, s = quantize_runq(x, gs)
+        assert np.array_equal(q, rq) and np.array_equal(s, rs)
+
+
+def matvec4(w, s, xq, xs, n, d, bits):
+    out = np.empty(d, np.float32)
+    oracle().or_matvec4(ptr(out), ptr(w), ptr(s), ptr(xq), ptr(xs), n, d, bits)
+    return out
+
+
+@pytest.mark.parametrize("k", range(5))
+def test_matvec4_golden(k):
+    n, d, bits = (int(v) for v in OPS[f"m{k}_shape"])
+    out = matvec4(OPS[f"m{k}_w"], OPS[f"m{k}_s"], OPS[f"m{k}_xq"], OPS[f"m{k}_xs"], n, d, bits)
+    assert np.array_equal(out.view(np.uint32), OPS[f"m{k}_out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_matvec4_groups_brute_force(bits):
+    rng = np.random.default_rng(11)
+    n, d = 256, 9
+    w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
+    xq = rng.integers(-128, 128, size=n, dtype=np.int8)
+    iv = np.empty((d, n // 32), np.int32)
+    oracle().or_matvec4_groups(ptr(iv), ptr(w), ptr(xq), n, d, bits)
+    wv = unpack_q4(w, d, n) if bits == 4 else w.view(np.int8).reshape(d, n).astype(np.int16)
+    want = (wv.reshape(d, n // 32, 32).astype(np.int64) * xq.reshape(1, n // 32, 32)).sum(2)
+    assert np.array_equal(iv, want)
+
+
+def test_matvec4_unit_scales_give_the_integer_sum():
+    rng = np.random.default_rng(5)
+    n, d = 32, 40
+    w = rng.integers(0, 256, size=d * n // 2, dtype=np.uint8)
+    s = np.full(d, 0x3C00, np.uint16)  # fp16 1.0
+    xq = rng.integers(-128, 128, size=n, dtype=np.int8)
+    out = matvec4(w, s, xq, np.ones(1, np.float32), n, d, 4)
+    want = (unpack_q4(w, d, n).astype(np.int64) * xq).sum(1)
+    assert np.array_equal(out, want.astype(np.float32))
+
+
+def test_matvec4_tolerance_bar_of_the_testbench():
+    rng = np.random.default_rng(13)
+    n, d = 896, 64
+    w = rng.integers(0, 256, size=d * n // 2, dtype=np.uint8)
+    s = f16_scales(rng, d * n // 32)
+    xq = rng.integers(-128, 128, size=n, dtype=np.int8)
+    xs = rng.uniform(1e-3, 1e-1, size=n // 32).astype(np.float32)
+    out = matvec4(w, s, xq, xs, n, d, 4)
+    ref, mag, _ = exact_terms(unpack_q4(w, d, n), s.view(np.float16).astype(np.float32), xq, xs)
+    assert (np.abs(out - ref) <= 1e-5 * mag).all()
+
+
+@pytest.mark.parametrize("k", range(3))
+def test_matvec_runq_golden(k):
+    n, d, gs = (int(v) for v in OPS[f"r{k}_shape"])
+    out = np.empty(d, np.float32)
+    oracle().or_matvec_runq(ptr(out), ptr(OPS[f"r{k}_wq"]), ptr(OPS[f"r{k}_ws"]), ptr(OPS[f"r{k}_xq"]),
+                            ptr(OPS[f"r{k}_xs"]), n, d, gs)
+    assert np.array_equal(out.view(np.uint32), OPS[f"r{k}_out"].view(np.uint32))
+
+
+def test_elementwise_against_reference_live():
+    Q = ref_lib("qwen")
+    if Q is None:
+        pytest.skip("oracle/_ref not built")
+    L = oracle()
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(896).astype(np.float32)
+    w = rng.standard_normal(896).astype(np.float32)
+    a, b = np.empty_like(x), np.empty_like(x)
+    L.or_rmsnorm(ptr(a), ptr(x), ptr(w), 896, C.c_float(1e-6))
+    Q.refq_rmsnorm(ptr(b), ptr(x), ptr(w), C.c_int(896), C.c_float(1e-6))
+    assert np.array_equal(a, b)
+    y1, y2 = x.copy(), x.copy()
+    L.or_softmax(ptr(y1), 896)
+    Q.refq_softmax(ptr(y2), C.c_int(896))
+    assert np.array_equal(y1, y2)
+    c, s = np.empty(32, np.float32), np.empty(32, np.float32)
+    L.or_rope_angles(ptr(c), ptr(s), 64, 77, C.c_float(1e6))
+    v1, v2 = x[:14 * 64].copy(), x[:14 * 64].copy()
+    L.or_rope_neox(ptr(v1), 14, 64, ptr(c), ptr(s))
+    Q.refq_rope(ptr(v2), C.c_int(14), C.c_int(64), ptr(c), ptr(s))
+    assert np.array_equal(v1, v2)
+    Q.refq_argmax.restype = C.c_int
+    p = np.array([1, 3, 3, 2], np.float32)
+    assert L.or_argmax(ptr(p), 4) == 1 == Q.refq_argmax(ptr(p), C.c_int(4))
+
+
+def test_rope_at_position_zero_is_identity():
+    L = oracle()
+    c, s = np.empty(32, np.float32), np.empty(32, np.float32)
+    L.or_rope_angles(ptr(c), ptr(s), 64, 0, C.c_float(1e6))
+    assert (c == 1).all() and (s == 0).all()
+    v = np.random.default_rng(4).standard_normal(128).astype(np.float32)
+    v2 = v.copy()
+    L.or_rope_neox(ptr(v2), 2, 64, ptr(c), ptr(s))
+    assert np.array_equal(v, v2)
+    q, k = v.copy(), v[:64].copy()
+    L.or_rope_runq(ptr(q), ptr(k), 128, 64, 32, 0)
+    assert np.array_equal(q, v) and np.array_equal(k, v[:64])
+
+
+def test_rope_runq_rotates_pairs():
+    # pos 1, head size 2: a single pair rotated by exactly 1 radian (freq = 1/10000^0 = 1)
+    L = oracle()
+    q = np.array([1.0, 0.0], np.float32)
+    k = np.array([0.0, 1.0], np.float32)
+    L.or_rope_runq(ptr(q), ptr(k), 2, 2, 2, 1)
+    c, s = np.cos(np.float32(1)), np.sin(np.float32(1))
+    assert np.allclose(q, [c, s], atol=1e-7) and np.allclose(k, [-s, c], atol=1e-7)
+
+
+def load_golden_logits(name, n):
+    return np.fromfile(os.path.join(GOLDEN, f"tiny_{name}_ref.logits"), dtype="<f4").reshape(-1, n)
+
+
+def replay_logits(m, prompt, ref):
+    """oracle logits along the reference's own token path: prompt, then its greedy choices"""
+    seq = list(prompt)
+    out = []
+    for pos in range(len(ref)):
+        out.append(m.forward(seq[pos], pos))
+        if pos + 1 >= len(seq):
+            seq.append(int(m.head_ids[int(np.argmax(ref[pos]))]))
+    return np.array(out)
+
+
+def test_whole_model_qwb_matches_reference_bit_exactly():
+    meta = json.load(open(os.path.join(GOLDEN, "tiny_ref.json")))["qwb"]
+    m = OracleModel(os.path.join(GOLDEN, "tiny.qwb"), meta["ctx"])
+    ref = load_golden_logits("qwb", m.n)
+    got = replay_logits(m, meta["prompt"], ref)
+    assert np.array_equal(got, ref)
+    m.close()
+    m = OracleModel(os.path.join(GOLDEN, "tiny.qwb"), meta["ctx"])
+    assert list(m.generate(meta["prompt"], meta["n"])) == meta["ids"]
+    m.close()
+
+
+def test_whole_model_bin_matches_reference_bit_exactly():
+    meta = json.load(open(os.path.join(GOLDEN, "tiny_ref.json")))["bin"]
+    m = OracleModel(os.path.join(GOLDEN, "tiny.bin"))
+    ref = load_golden_logits("bin", m.n)
+    got = replay_logits(m, meta["prompt"], ref)
+    assert np.array_equal(got, ref)
+    m.close()
+    m = OracleModel(os.path.join(GOLDEN, "tiny.bin"))
+    assert list(m.generate(meta["prompt"], meta["steps"])) == meta["ids"]
+    m.close()
+
+
+def test_sampler_matches_reference_stream():
+    """temperature + top-p with the xorshift coin: the reference binary's sampled ids (-t 0.9 -p 0.9 -s 42)"""
+    meta = json.load(open(os.path.join(GOLDEN, "tiny_ref.json")))["qwb_sampled"]
+    m = OracleModel(os.path.join(GOLDEN, "tiny.qwb"), meta["ctx"])
+    rng = C.c_ulonglong(meta["seed"])
+    token, out = meta["prompt"][0], []
+    for pos in range(meta["ctx"]):
+        lg = m.forward(token, pos)
+        if pos < len(meta["prompt"]) - 1:
+            token = meta["prompt"][pos + 1]
+            continue
+        row = oracle().or_sample(ptr(lg), m.n, C.c_float(meta["t"]), C.c_float(meta["p"]), C.byref(rng))
+        nxt = int(m.head_ids[row])
+        out.append(nxt)
+        if len(out) >= meta["n"]:
+            break
+        token = nxt
+    m.close()
+    assert out == meta["ids"]
+
+
+def test_xorshift_first_values():
+    # xorshift64* (Marsaglia shifts 12/25/27, Vigna's multiplier), first outputs from state 1 by hand
+    L = oracle()
+    st = C.c_ulonglong(1)
+    x, want = 1, []
+    for _ in range(3):
+        x ^= x >> 12
+        x ^= (x << 25) & 0xFFFFFFFFFFFFFFFF
+        x ^= x >> 27
+        want.append(((x * 0x2545F4914F6CDD1D) & 0xFFFFFFFFFFFFFFFF) >> 32)
+    got = [L.or_random_u32(C.byref(st)) for _ in range(3)]
+    assert got == want
+
+
+def test_reordering_the_group_sum_alone_moves_logits_by_int8_boundary_flips(tmp_path):
+    """Tolerance rationale for the free-running model comparisons.  The reference's own arithmetic, with
+    nothing changed but the order of the fp32 sum over a row's groups (4 partial sums instead of one
+    chain), drifts from the sequential result by whole int8 steps wherever a re-quantized activation sat
+    within rounding of a boundary: positions are either exact to ~1e-6 or jump to 1e-4..1e-2."""
+    from helpers import synth
+    p = synth("qwb", str(tmp_path / "c5l1.qwb"), "c5", 22, "layers=1", "vocab=8192", "head_k=8192")
+    L = oracle()
+    toks = [int(v) for v in np.random.default_rng(6).integers(0, 8192, 8)]
+    errs = []
+    try:
+        a, b = OracleModel(p, 32), OracleModel(p, 32)
+        for pos, t in enumerate(toks):
+            L.or_set_sum_ways(1)
+            la = a.forward(t, pos)
+            L.or_set_sum_ways(4)
+            lb = b.forward(t, pos)
+            errs.append(float(np.abs(lb - la).max() / np.abs(la).max()))
+    finally:
+        L.or_set_sum_ways(1)
+    a.close()
+    b.close()
+    exact = [e for e in errs if e < 1e-5]
+    jumps = [e for e in errs if e >= 1e-4]
+    assert exact and jumps, errs
+    assert len(exact) + len(jumps) == len(errs), errs  # nothing in between: discrete events
+    assert max(errs) < 2e-2, errs
