@@ -1,0 +1,212 @@
+"""Decode benchmark of the device-resident token loop (one MI355X).
+
+Workload (the configuration the headline metric is quoted on): Qwen2-0.5B shape, .qwb with Q4_0 layer
+planes (dim 896, 24 layers, 14 query / 2 KV heads, FFN 4864, RoPE theta 1e6) and a 65536-row Q8_0 head
+with seeded head_ids; seeded N(0, 0.02) random-init weights written by host/synth; 24-token seeded prompt,
+greedy, batch 1.  A step is one decode position: the whole forward() plus the argmax on the device, one
+hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
+
+  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c3|c5] [--no-cpu]
+
+Also reported: per-kernel roofline (HIP events around every launch on the library's stream, algorithmic
+bytes per launch), the greedy ids against the reference's own qwen.c, and that qwen.c (built with OpenMP,
+-O3 -ffast-math, oracle/_ref/qwen_fast) timed on this host's cores on a bounded sample of the workload."""
+import argparse
+import importlib.util
+import json
+import os
+import re
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "local-llama-pynq-z2_amd")
+PEAK_HBM = 8000.0  # GB/s, MI355X
+CONFIGS = {
+    "c3": dict(preset="c3", seed=3, prompt=24, new=128, ctx=1024,
+               workload="Qwen2-0.5B shape .qwb decode (dim 896, 24 layers, 14/2 heads, FFN 4864, Q4_0 layers, "
+                        "Q8_0 65536-row head): 24-token prompt, 128 greedy tokens, batch 1"),
+    "c5": dict(preset="c5", seed=5, prompt=32, new=256, ctx=4096,
+               workload="Qwen2-7B shape .qwb decode (dim 3584, 28 layers, 28/4 heads of 128, FFN 18944, Q4_0 "
+                        "layers, Q8_0 152064-row head): 32-token prompt, 256 greedy tokens, KV cache 4096, batch 1"),
+}
+
+
+def load_pkg():
+    spec = importlib.util.spec_from_file_location("llm_hip", os.path.join(PKG, "__init__.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def model_file(cfg):
+    d = os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, f"{cfg['preset']}_s{cfg['seed']}.qwb")
+    if not os.path.exists(path):
+        t = time.time()
+        subprocess.run([os.path.join(PKG, "host", "synth"), "qwb", path + ".tmp", cfg["preset"], str(cfg["seed"])],
+                       check=True, capture_output=True)
+        os.replace(path + ".tmp", path)
+        log(f"wrote {path} ({os.path.getsize(path) / 2**20:.0f} MiB) in {time.time() - t:.1f} s")
+    return path
+
+
+def head_ids_of(path):
+    with open(path, "rb") as f:
+        b = f.read(256)
+    dim, hid, L, nh, nkv, vocab, head_k = np.frombuffer(b, np.int32, 7, 8)
+    kv = dim // nh * nkv
+    pad = lambda n: (n + 63) & ~63
+    off = 256 + pad(4 * dim) * 3 * L + pad(4 * kv) * 2 * L + pad(4 * dim)
+    return np.fromfile(path, np.int32, int(head_k), offset=off)
+
+
+def cpu_baseline(path, prompt, n_new, ctx):
+    """the reference's qwen.c (OpenMP build) on this host: bounded sample of the same workload"""
+    exe = os.path.join(REPO, "oracle", "_ref", "qwen_fast")
+    if not os.path.exists(exe):
+        return None
+    threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+    t = time.time()
+    r = subprocess.run([exe, path, "--ids", ",".join(map(str, prompt)), "-t", "0", "-n", str(n_new), "-c", str(ctx)],
+                       capture_output=True, text=True, env=env, timeout=600)
+    wall = time.time() - t
+    m = re.search(r"generated: (\d+) tokens, ([0-9.]+) tok/s", r.stderr)
+    if r.returncode != 0 or not m:
+        log(f"cpu baseline failed: {r.stderr[-400:]}")
+        return None
+    return {"value": float(m.group(2)), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"qwen.c (OpenMP, -O3 -ffast-math -march=x86-64-v3) on the same .qwb: {len(prompt)}-token "
+                      f"prompt + {int(m.group(1))} greedy tokens, decode rate as qwen.c prints it ({wall:.1f} s wall)"}
+
+
+def greedy_parity(path, prompt, n_new, ctx, ids_gpu, logits_gpu):
+    """the reference's qwen.c built strict IEEE (oracle/_ref/qwen): its greedy ids and --logits dump against
+    the device run; a divergence is reported with the reference's top-2 logit gap at that position"""
+    exe = os.path.join(REPO, "oracle", "_ref", "qwen")
+    if not os.path.exists(exe):
+        return None
+    dump = os.path.join(os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench"), "ref.logits")
+    threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
+    r = subprocess.run([exe, path, "--ids", ",".join(map(str, prompt)), "-t", "0", "-n", str(n_new), "-c", str(ctx),
+                        "--logits", dump], capture_output=True, text=True, timeout=900,
+                       env=dict(os.environ, OMP_NUM_THREADS=str(threads)))
+    if r.returncode != 0:
+        return None
+    ids_ref = [int(v) for v in r.stdout.strip().split(",") if v]
+    ref = np.fromfile(dump, np.float32).reshape(-1, logits_gpu.shape[1])
+    n = min(len(ids_ref), len(ids_gpu))
+    div = next((i for i in range(n) if ids_ref[i] != ids_gpu[i]), None)
+    rows = min(len(ref), len(logits_gpu))
+    upto = rows if div is None else len(prompt) + div  # positions on the shared token path
+    errs = [float(np.abs(logits_gpu[p] - ref[p]).max() / np.abs(ref[p]).max()) for p in range(upto)]
+    out = {"reference": "qwen.c strict IEEE build", "tokens_compared": n, "identical": div is None,
+           "first_divergence": div, "logit_rel_err_max": max(errs) if errs else None,
+           "logit_rel_err_median": float(np.median(errs)) if errs else None}
+    if div is not None:
+        row = ref[len(prompt) - 1 + div]
+        top = np.sort(row)[-2:]
+        out["reference_top2_gap_rel"] = float((top[1] - top[0]) / np.abs(row).max())
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--profile-steps", type=int, default=32)
+    ap.add_argument("--cpu-tokens", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    cfg = CONFIGS[a.config]
+    steps = a.steps or cfg["new"]
+    path = model_file(cfg)
+    hid = head_ids_of(path)
+    prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).choice(hid, cfg["prompt"], replace=False)]
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    torch.cuda.init()
+    P = load_pkg()
+    t = time.time()
+    m = P.Model(path, cfg["ctx"])
+    log(f"model resident in {time.time() - t:.1f} s: {m.info.weight_bytes / 2**20:.0f} MiB of tiled weights, "
+        f"{m.info.gemv_bytes_per_token / 1e6:.2f} MB GEMV bytes per token")
+    if len(prompt) + 1 + max(steps, a.warmup, a.profile_steps) >= m.info.ctx:
+        raise SystemExit("steps do not fit the context")
+
+    # greedy run of the workload (also the parity line against the reference below)
+    gen = m.generate(prompt, steps, logits=True)
+    ids_gpu = [int(v) for v in gen["ids"]]
+    log(f"greedy run: {len(ids_gpu)} tokens, device decode {gen['timing'].decode_ms:.1f} ms "
+        f"({(gen['timing'].n_forward - len(prompt)) / gen['timing'].decode_ms * 1e3:.0f} tok/s with host stop checks)")
+
+    # warmup: W steps after the prompt, then back to the prompt's end for the timed steps
+    m.generate(prompt, 1)
+    if a.warmup:
+        m.decode_replay(a.warmup)
+    m.generate(prompt, 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev_ms = m.decode_replay(steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    tok_s = steps / wall
+    log(f"timed {steps} decode steps: {wall * 1e3:.2f} ms wall, {ev_ms:.2f} ms by events -> {tok_s:.1f} tok/s")
+
+    # per-kernel roofline (HIP events on the library's stream)
+    m.generate(prompt, 1)
+    stats = m.profile(a.profile_steps)
+    total = sum(s["total_ms"] for s in stats)
+    for s in sorted(stats, key=lambda s: -s["total_ms"]):
+        avg = s["total_ms"] / s["launches"]
+        log(f"  {s['name']:12s} {s['launches']:6d} launches  avg {avg * 1e3:8.2f} us  {s['total_ms'] / total * 100:5.1f}%"
+            f"  {s['bytes_per_launch'] / 1e6:8.3f} MB  {s['bytes_per_launch'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
+    dom = max(stats, key=lambda s: s["total_ms"])
+    dom_avg_s = dom["total_ms"] / dom["launches"] * 1e-3
+    achieved = dom["bytes_per_launch"] / dom_avg_s / 1e9
+    gemv = [s for s in stats if s["name"].endswith("_gemv")]
+    gemv_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in gemv)
+    gemv_s = sum(s["total_ms"] for s in gemv) * 1e-3
+    m.close()
+
+    cpu = None if a.no_cpu else cpu_baseline(path, prompt, a.cpu_tokens, cfg["ctx"])
+    match = None if a.no_cpu else greedy_parity(path, prompt, a.cpu_tokens, cfg["ctx"], ids_gpu, gen["logits"])
+
+    out = {
+        "metric": "decode tok/s + GEMV HBM GB/s (% of peak), Q4_0 Qwen2-0.5B shape, batch 1",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) random-init weights (Q4_0 layers, Q8_0 head), seeded prompt ids",
+        "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
+                   "ctx": cfg["ctx"], "batch": 1},
+        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                     "avg_launch_us": round(dom_avg_s * 1e6, 3), "bytes_per_launch": round(dom["bytes_per_launch"])},
+        "gemv_all": {"achieved": round(gemv_bytes / gemv_s / 1e9, 1), "unit": "GB/s",
+                     "frac": round(gemv_bytes / gemv_s / 1e9 / PEAK_HBM, 4),
+                     "share_of_step": round(sum(s["total_ms"] for s in gemv) / total, 4)},
+        "cpu_baseline": cpu,
+        "greedy_vs_reference": match,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

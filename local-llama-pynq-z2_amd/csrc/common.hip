@@ -3,20 +3,23 @@
 
 #include "host_common.h"
 
-// Shapes follow from the tiled matrix: a row-block has `nchunks` chunk records of 1 KiB+ each.  Long rows
-// (many chunks) split their chunks over several waves of a block (kw), short rows put several row-blocks
-// into one block (nb), so a block always has 4..16 waves.  Epilogues that need whole groups of rows in one
-// iteration fix nb: SwiGLU quantizes gs hidden values per group, each row-block yields rb/2 of them.
+// Shapes follow from the tiled matrix: a row-block has `nchunks` chunk records of 1 KiB+ each.  The chunks of
+// a row-block are split over kw waves so that each wave holds at most a few batches, and one block takes
+// one iteration (row-blocks of one block: nb), so that the whole grid's loads are in flight at once and a
+// block's latency chain is one load round trip plus its prologue.  Epilogues that need whole groups of rows
+// fix nb: SwiGLU quantizes gs hidden values per group, each row-block yields rb/2 of them.
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered) {
+    (void)pro;
     GemvShape s;
     const int C = T.nchunks;
     if (ordered) {
         s.kw = 1;
         s.nb = 4;
     } else {
-        s.kw = C >= 48 ? 8 : C >= 16 ? 4 : C >= 6 ? 2 : 1;
-        s.nb = 8 / s.kw > 0 ? 8 / s.kw : 1;
-        if (s.nb < 1) s.nb = 1;
+        s.kw = (C + 3) / 4;
+        if (s.kw > 16) s.kw = 16;
+        if (s.kw < 1) s.kw = 1;
+        s.nb = 4 / s.kw > 1 ? 4 / s.kw : 1;
     }
     if (epi == EPI_SWIGLU) {
         s.nb = T.gs / (T.rb / 2);
@@ -24,12 +27,13 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered) {
         if (s.kw < 1) s.kw = 1;
     }
     const int iters = (T.nblocks + s.nb - 1) / s.nb;
-    // blocks that normalize x first keep that prologue rare: at most ~2 blocks per CU
-    const int cap = pro == PRO_NORM || pro == PRO_ATTN ? 512 : 4096;
-    s.grid = iters < cap ? iters : cap;
+    s.grid = iters < 65535 ? iters : 65535;
     if (s.grid < 1) s.grid = 1;
     return s;
 }
+
+// Long rows with few of them (a down projection) take 8-row blocks, so that the grid still covers the chip.
+int gemv_row_block(int d, int n) { return n >= 4096 && d <= 8192 ? 8 : 16; }
 
 int stream_wait(hipStream_t st, long timeout_ms, const char *who) {
     struct timespec t0, t;

@@ -36,6 +36,8 @@ struct GemvShape {
     int kw, nb, grid;
 };
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered);
+// Row-block size for a plain matrix of d rows x n inputs (fused QKV and gate/up keep 16 for their pairing).
+int gemv_row_block(int d, int n);
 
 // Wait for the stream with a time limit (the reference's 5 s ap_done poll, matvec_fpga.cpp:193-207).
 // Returns 0, 1 on time-out, -1 on a HIP error (message printed).

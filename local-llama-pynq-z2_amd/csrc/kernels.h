@@ -16,6 +16,20 @@ struct StepCtrl {
     int pad[3];
 };
 
+// Attention positions are processed in sub-chunks of this many rows (LDS staging of K and V).
+#define ATT_SUB 32
+
+// Position slices of one attention step: P = pos + 1 positions in S = min(splits, ceil(P / ATT_SUB)) slices
+// of `chunk` positions (the attention kernel and the o-projection's merge use the same split).
+__device__ __forceinline__ void att_slices(int pos, int splits, int *S, int *chunk) {
+    const int P = pos + 1;
+    int s = (P + ATT_SUB - 1) / ATT_SUB;
+    if (s > splits) s = splits;
+    *S = s;
+    *chunk = (P + s - 1) / s;
+}
+
+
 // Prologues: how the int8 activation vector reaches LDS.
 enum { PRO_XQ = 0, PRO_NORM = 1, PRO_ATTN = 2 };
 // Epilogues: what happens to the finished rows.
@@ -38,7 +52,7 @@ struct GemvArgs {
     // PRO_ATTN: combine split attention partials -> quantize
     const float *att_ml;    // [n_heads][splits][2] (max score, sum of exp)
     const float *att_acc;   // [n_heads][splits][hs]
-    int n_heads, head_size, att_splits, att_chunk;
+    int n_heads, head_size, att_splits;
     // EPI_STORE / EPI_RESID / EPI_ARGMAX: out[row] (= or +=)
     float *out;
     // EPI_ARGMAX
@@ -60,7 +74,7 @@ struct AttnArgs {
     const float *q;         // [n_heads * hs]
     const float *kc, *vc;   // layer bases [ctx][kv_dim]
     float *ml, *acc;        // partials, see GemvArgs
-    int n_heads, n_kv, hs, kv_dim, chunk, splits;
+    int n_heads, n_kv, hs, kv_dim, splits; // splits: maximum number of position slices (grid)
     const StepCtrl *ctrl;
 };
 
@@ -72,6 +86,12 @@ struct EmbedArgs {
     StepCtrl *ctrl;
     const int *prompt;      // generate mode
     int *tokens;            // [ctx] input token of every position
+    // generate mode: the previous step's argmax partials, finished here
+    const float *pv;
+    const int *pi;
+    int np;
+    const int *head_ids;    // NULL: identity
+    int *gen;               // [ctx] argmax result of every position
 };
 
 struct ArgmaxArgs {

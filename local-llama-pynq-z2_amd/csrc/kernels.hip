@@ -53,14 +53,15 @@ __device__ __forceinline__ int seg_dot(const uint4 *wv, const uint32_t *x) {
 // ------------------------------------------------------------------------------------------------------
 // GEMV
 
+// Per-format constants.  A batch (the loads one wave keeps in flight per buffer) is 4 KiB of weights:
+// 4 chunks of int4 x 32, 2 of int8 x 32, 1 of int8 x 64, so registers stay bounded in every format.
 template <int WB, int GSZ, int SF32>
 struct Fmt {
     static constexpr int SB = GSZ * WB / 8; // bytes per (row, group) segment
     static constexpr int PIECES = SB / 16;
     static constexpr int SCB = SF32 ? 4 : 2;
+    static constexpr int UNROLL = 4 / PIECES;
 };
-
-#define UNROLL 4
 
 __device__ __forceinline__ float rope_pair_out(float self, float partner, bool first, float c, float s) {
     // qwen.c:483-485 / runq.c:516-519: first = a*c - b*s, second = b*c + a*s (a first, b second element)
@@ -70,6 +71,56 @@ __device__ __forceinline__ float rope_pair_out(float self, float partner, bool f
     }
     float t1 = self * c, t2 = partner * s;
     return t1 + t2;
+}
+
+template <int WB, int GSZ, int SF32>
+__device__ __forceinline__ void load_batch(const uint8_t *base, size_t rec_bytes, int nchunks, int c0, int kw, int lane,
+                                           uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
+                                           uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+    using F = Fmt<WB, GSZ, SF32>;
+#pragma unroll
+    for (int u = 0; u < F::UNROLL; u++) {
+        const int c = c0 + u * kw;
+        if (c < nchunks) {
+            const uint8_t *rec = base + (size_t)c * rec_bytes;
+#pragma unroll
+            for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
+            if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
+            else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
+        }
+    }
+}
+
+// groups of one batch, added to the lane's running sum in chunk order: p_g = ((float)ival * ws) * xs
+template <int WB, int GSZ, int SF32>
+__device__ __forceinline__ float use_batch(float acc, int nchunks, int c0, int kw, int gpc, int g_lane, const int8_t *sxq,
+                                           const float *sxs,
+                                           const uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
+                                           const uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+    using F = Fmt<WB, GSZ, SF32>;
+#pragma unroll
+    for (int u = 0; u < F::UNROLL; u++) {
+        const int c = c0 + u * kw;
+        if (c < nchunks) {
+            const int g = c * gpc + g_lane;
+            const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
+            const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
+            float p = (float)iv * sc; // qwen.c:452, runq.c:452
+            p = p * sxs[g];
+            acc = acc + p;
+        }
+    }
+    return acc;
+}
+
+// Logical row R of the fused QKV matrix with NeoX pairing: element, partner element, frequency index.
+__device__ __forceinline__ void qkv_neox_row(int R, int hs, int *e, int *ep, int *i, bool *first) {
+    const int half = hs / 2, blk = R / 16, r = R & 15, per = half / 8;
+    const int hh = blk / per;
+    *i = (blk - hh * per) * 8 + (r & 7);
+    *first = r < 8;
+    *e = hh * hs + (r < 8 ? *i : half + *i);
+    *ep = hh * hs + (r < 8 ? half + *i : *i);
 }
 
 template <int WB, int GSZ, int SF32, int PRO, int EPI>
@@ -85,9 +136,52 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     float *sred = sxs + ngp;                              // nw * 64
     float *srow = sred + nw * WAVE;                       // nb * rb
     float *sv = srow + a.nb * rb;                         // prologue / epilogue floats
-    const int pos = (PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX) ? a.ctrl->pos : 0;
+    const int my_nb = wave / a.kw, my_kw = wave - my_nb * a.kw;
+    const int rows_it = a.nb * rb;
+    const int n_it = (W.nblocks + a.nb - 1) / a.nb;
+    const int g_lane = lane / rb;
+    const int it0 = blockIdx.x;
 
-    // ---- prologue: int8 activations and their scales into LDS
+    // (1) weights of this block's first iteration: the first batch is issued before anything else
+    uint4 wa[F::UNROLL][F::PIECES], wb[F::UNROLL][F::PIECES];
+    uint32_t sa[F::UNROLL], sb[F::UNROLL];
+    {
+        const int b = it0 * a.nb + my_nb;
+        if (it0 < n_it && b < W.nblocks)
+            load_batch<WB, GSZ, SF32>(W.data + (size_t)b * W.nchunks * W.rec, W.rec, W.nchunks, my_kw, a.kw, lane, wa, sa);
+    }
+    // (2) the step's position and the epilogue operands of this thread's first row
+    const bool need_pos = PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX;
+    const int pos = need_pos ? a.ctrl->pos : 0;
+    float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f, pre_x = 0.0f;
+    {
+        const int R = it0 * rows_it + tid;
+        if (tid < rows_it && R < W.rows) {
+            if constexpr (EPI == EPI_RESID) pre_x = a.out[R];
+            if constexpr (EPI == EPI_QKV) {
+                const int half = a.head_size / 2;
+                if (a.rope_kind == ROPE_NEOX) {
+                    if (R < a.dim + a.kv_dim) {
+                        int e, ep, i;
+                        bool first;
+                        qkv_neox_row(R, a.head_size, &e, &ep, &i, &first);
+                        pre_b = a.bias[e];
+                        pre_bp = a.bias[ep];
+                        pre_c = a.rope_cos[(size_t)pos * half + i];
+                        pre_s = a.rope_sin[(size_t)pos * half + i];
+                    } else {
+                        pre_b = a.bias[R];
+                    }
+                } else if (R < a.dim + a.kv_dim) {
+                    const int e = R < a.dim ? R : R - a.dim, i = (e % a.head_size) / 2;
+                    pre_c = a.rope_cos[(size_t)pos * half + i];
+                    pre_s = a.rope_sin[(size_t)pos * half + i];
+                }
+            }
+        }
+    }
+
+    // (3) prologue: int8 activations and their scales into LDS
     if constexpr (PRO == PRO_XQ) {
         const uint32_t *src = (const uint32_t *)a.xq;
         uint32_t *dst = (uint32_t *)sxq;
@@ -96,32 +190,43 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     } else {
         if constexpr (PRO == PRO_NORM) {
             // rmsnorm (qwen.c:337-344, runq.c:394-407): ss = sum x^2; ss /= n; ss += eps; ss = 1/sqrtf(ss)
+            // x and the gains are read in one pass (gains parked in the upper half of sv)
             float part = 0.0f;
             for (int i = tid; i < n; i += nt) {
-                float v = a.x[i];
+                const float v = a.x[i], w = a.norm_w[i];
                 sv[i] = v;
+                sv[n + i] = w;
                 part += v * v;
             }
             float ss = block_sum(part, sred);
             ss /= (float)n;
             ss += a.eps;
             ss = 1.0f / sqrtf(ss);
-            for (int i = tid; i < n; i += nt) sv[i] = a.norm_w[i] * (ss * sv[i]);
-        } else { // PRO_ATTN: merge the split softmax partials of every head, then xb = acc / l
-            const int hs = a.head_size, S = a.att_splits;
-            const int active = min(S, pos / a.att_chunk + 1);
+            for (int i = tid; i < n; i += nt) sv[i] = sv[n + i] * (ss * sv[i]);
+        } else { // PRO_ATTN: merge the attention slices of every head (weights in LDS), then xb = acc / l
+            const int hs = a.head_size, SP = a.att_splits, nh = a.n_heads;
+            int S, chunk;
+            att_slices(pos, SP, &S, &chunk);
+            float *wgt = sv + n; // nh * S merge weights
+            for (int h = tid; h < nh; h += nt) {
+                const float *ml = a.att_ml + (size_t)h * SP * 2;
+                float m = ml[0];
+                for (int k = 1; k < S; k++) m = fmaxf(m, ml[2 * k]);
+                float l = 0.0f;
+                for (int k = 0; k < S; k++) {
+                    const float f = expf(ml[2 * k] - m);
+                    wgt[h * S + k] = f;
+                    l += ml[2 * k + 1] * f;
+                }
+                const float inv = 1.0f / l;
+                for (int k = 0; k < S; k++) wgt[h * S + k] *= inv;
+            }
+            __syncthreads();
             for (int i = tid; i < n; i += nt) {
                 const int h = i / hs, e = i - h * hs;
-                const float *ml = a.att_ml + (size_t)h * S * 2;
-                float m = ml[0];
-                for (int s = 1; s < active; s++) m = fmaxf(m, ml[2 * s]);
-                float l = 0.0f, v = 0.0f;
-                for (int s = 0; s < active; s++) {
-                    float f = expf(ml[2 * s] - m);
-                    l += ml[2 * s + 1] * f;
-                    v += a.att_acc[((size_t)h * S + s) * hs + e] * f;
-                }
-                sv[i] = v / l;
+                float v = 0.0f;
+                for (int k = 0; k < S; k++) v += a.att_acc[((size_t)h * SP + k) * hs + e] * wgt[h * S + k];
+                sv[i] = v;
             }
         }
         __syncthreads();
@@ -131,44 +236,24 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     }
     __syncthreads();
 
-    // ---- main loop over groups of nb row-blocks
-    const int my_nb = wave / a.kw, my_kw = wave - my_nb * a.kw;
-    const int rows_it = a.nb * rb;
-    const int n_it = (W.nblocks + a.nb - 1) / a.nb;
+    // (4) main loop over iterations (usually one per block), batches double-buffered
     float best_v = -INFINITY;
     int best_i = 0x7fffffff;
-    for (int it = blockIdx.x; it < n_it; it += gridDim.x) {
+    for (int it = it0; it < n_it; it += gridDim.x) {
         const int b = it * a.nb + my_nb;
         float acc = 0.0f;
         if (b < W.nblocks) {
             const uint8_t *base = W.data + (size_t)b * W.nchunks * W.rec;
-            const int g_lane = lane / rb;
-            for (int c0 = my_kw; c0 < W.nchunks; c0 += a.kw * UNROLL) {
-                uint4 wv[UNROLL][F::PIECES];
-                uint32_t sr[UNROLL];
-#pragma unroll
-                for (int u = 0; u < UNROLL; u++) {
-                    const int c = c0 + u * a.kw;
-                    if (c < W.nchunks) {
-                        const uint8_t *rec = base + (size_t)c * W.rec;
-#pragma unroll
-                        for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
-                        if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
-                        else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < UNROLL; u++) {
-                    const int c = c0 + u * a.kw;
-                    if (c < W.nchunks) {
-                        const int g = c * gpc + g_lane;
-                        const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
-                        const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
-                        float p = (float)iv * sc; // qwen.c:452, runq.c:452: ((float)ival * ws) * xs
-                        p = p * sxs[g];
-                        acc = acc + p;
-                    }
-                }
+            const int step = a.kw * F::UNROLL;
+            if (it != it0) load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, my_kw, a.kw, lane, wa, sa);
+            for (int c0 = my_kw;; c0 += 2 * step) {
+                if (c0 + step < W.nchunks) load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, c0 + step, a.kw, lane, wb, sb);
+                acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, c0, a.kw, gpc, g_lane, sxq, sxs, wa, sa);
+                if (c0 + step >= W.nchunks) break;
+                if (c0 + 2 * step < W.nchunks)
+                    load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, c0 + 2 * step, a.kw, lane, wa, sa);
+                acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, c0 + step, a.kw, gpc, g_lane, sxq, sxs, wb, sb);
+                if (c0 + 2 * step >= W.nchunks) break;
             }
         }
         acc = wave_sum_from(acc, rb); // lanes holding the same row
@@ -184,10 +269,11 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
 
         // ---- epilogue
         const int R = it * rows_it + tid; // logical row of this thread
+        const bool first_it = it == it0;
         if constexpr (EPI == EPI_STORE) {
             if (tid < rows_it && R < W.rows) a.out[R] = srow[tid];
         } else if constexpr (EPI == EPI_RESID) {
-            if (tid < rows_it && R < W.rows) a.out[R] += srow[tid]; // qwen.c:551, 565
+            if (tid < rows_it && R < W.rows) a.out[R] = (first_it ? pre_x : a.out[R]) + srow[tid]; // qwen.c:551, 565
         } else if constexpr (EPI == EPI_ARGMAX) {
             if (tid < rows_it && R < W.rows) {
                 const float v = srow[tid];
@@ -198,35 +284,42 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
         } else if constexpr (EPI == EPI_QKV) {
             if (tid < rows_it && R < W.rows) {
                 const int dim = a.dim, kvd = a.kv_dim, hs = a.head_size, half = hs / 2;
-                float v = srow[tid];
+                const float v = srow[tid];
                 if (a.rope_kind == ROPE_NEOX) {
                     // rows [0, dim + kv) hold q then k in blocks of 16: 8 first-half rows, then their 8 partners
                     if (R < dim + kvd) {
-                        const int blk = R / 16, r = R & 15, per = half / 8;
-                        const int hh = blk / per, i0 = (blk - hh * per) * 8, i = i0 + (r & 7);
-                        const int e = hh * hs + (r < 8 ? i : half + i);
-                        const int ep = hh * hs + (r < 8 ? half + i : i);
-                        float self = v + a.bias[e], partner = srow[tid ^ 8] + a.bias[ep];
-                        const float c = a.rope_cos[(size_t)pos * half + i], s = a.rope_sin[(size_t)pos * half + i];
-                        float o = rope_pair_out(self, partner, r < 8, c, s);
+                        int e, ep, i;
+                        bool first;
+                        qkv_neox_row(R, hs, &e, &ep, &i, &first);
+                        float bs = pre_b, bp = pre_bp, c = pre_c, sn = pre_s;
+                        if (!first_it) {
+                            bs = a.bias[e];
+                            bp = a.bias[ep];
+                            c = a.rope_cos[(size_t)pos * half + i];
+                            sn = a.rope_sin[(size_t)pos * half + i];
+                        }
+                        const float o = rope_pair_out(v + bs, srow[tid ^ 8] + bp, first, c, sn);
                         if (e < dim) a.q[e] = o;
                         else a.kc[(size_t)pos * kvd + (e - dim)] = o;
                     } else {
-                        const int e = R - dim - kvd;
-                        a.vc[(size_t)pos * kvd + e] = v + a.bias[dim + kvd + e];
+                        const float bs = first_it ? pre_b : a.bias[R];
+                        a.vc[(size_t)pos * kvd + (R - dim - kvd)] = v + bs;
                     }
                 } else {
                     // natural order q, k, v; pairs (2i, 2i+1) rotate (runq.c:506-521)
                     if (R < dim + kvd) {
                         const int e = R < dim ? R : R - dim;
                         const int i = (e % hs) / 2;
-                        const float c = a.rope_cos[(size_t)pos * half + i], s = a.rope_sin[(size_t)pos * half + i];
-                        const bool first = (e & 1) == 0;
+                        float c = pre_c, sn = pre_s;
+                        if (!first_it) {
+                            c = a.rope_cos[(size_t)pos * half + i];
+                            sn = a.rope_sin[(size_t)pos * half + i];
+                        }
                         const float partner = srow[tid ^ 1];
                         // first: v0*fcr - v1*fci; second: v0*fci + v1*fcr (v0 first, v1 second)
                         float o;
-                        if (first) { float t1 = v * c, t2 = partner * s; o = t1 - t2; }
-                        else { float t1 = partner * s, t2 = v * c; o = t1 + t2; }
+                        if ((e & 1) == 0) { float t1 = v * c, t2 = partner * sn; o = t1 - t2; }
+                        else { float t1 = partner * sn, t2 = v * c; o = t1 + t2; }
                         if (R < dim) a.q[e] = o;
                         else a.kc[(size_t)pos * kvd + e] = o;
                     } else {
@@ -283,7 +376,9 @@ size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
     const int ngp = W.nchunks * (WAVE / W.rb);
     size_t b = (size_t)ngp * W.gs + (size_t)ngp * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
     size_t extra = 0;
-    if (pro != PRO_XQ) extra = (size_t)W.n * 4;
+    if (pro == PRO_NORM) extra = (size_t)W.n * 8;
+    if (pro == PRO_ATTN) extra = (size_t)W.n * 4;
+    if (pro == PRO_ATTN) extra += (size_t)a.n_heads * a.att_splits * 4;
     if (epi == EPI_SWIGLU) extra = extra > (size_t)a.nb * W.rb * 2 ? extra : (size_t)a.nb * W.rb * 2;
     return b + extra + 16;
 }
@@ -318,93 +413,97 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
 }
 
 // ------------------------------------------------------------------------------------------------------
-// decode attention (qwen.c:526-546, runq.c:530-568), split over positions: block (kv head, split) covers
-// `chunk` positions for the kv_mul query heads that share the kv head; it writes the split's max score,
-// sum of exponentials and exp-weighted value sum, which the o-projection's prologue merges.
+// decode attention (qwen.c:526-546, runq.c:530-568), split over positions.  The P = pos+1 positions are
+// cut into S = min(splits, ceil(P/32)) equal slices; block (kv head, slice) holds the slice's K and V rows
+// in LDS 32 positions at a time and serves the kv_mul query heads that share the kv head.  It leaves the
+// slice's running max, sum of exponentials and exp-weighted value sum (online softmax), which the
+// o-projection's prologue merges.  Scores are sequential dot products in the reference's order.
 
 __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
     const int pos = a.ctrl->pos;
     const int kvh = blockIdx.x / a.splits, s = blockIdx.x - kvh * a.splits;
-    const int t0 = s * a.chunk;
-    if (t0 > pos) return;
-    const int T = min(a.chunk, pos + 1 - t0);
+    int S, chunk;
+    att_slices(pos, a.splits, &S, &chunk);
+    if (s >= S) return;
+    const int t_begin = s * chunk, t_end = min(t_begin + chunk, pos + 1);
     const int hs = a.hs, kv_mul = a.n_heads / a.n_kv, tid = threadIdx.x, nt = blockDim.x;
     const int wave = tid / WAVE, lane = tid & (WAVE - 1), nw = nt / WAVE;
-    float *sq = sm;                       // kv_mul * hs
-    float *sc = sq + kv_mul * hs;         // kv_mul * chunk
-    float *sp = sc + kv_mul * a.chunk;    // partial sums: slices * kv_mul * hs
-    const float *K = a.kc + (size_t)t0 * a.kv_dim + (size_t)kvh * hs;
-    const float *V = a.vc + (size_t)t0 * a.kv_dim + (size_t)kvh * hs;
-    for (int i = tid; i < kv_mul * hs; i += nt) sq[i] = a.q[(size_t)kvh * kv_mul * hs + i];
-    __syncthreads();
-    // scores: score = (q . k) / sqrtf(hs)
+    float *sq = sm;                          // kv_mul * hs
+    float *sk = sq + kv_mul * hs;            // ATT_SUB * hs
+    float *sv = sk + ATT_SUB * hs;           // ATT_SUB * hs
+    float *sc = sv + ATT_SUB * hs;           // kv_mul * ATT_SUB scores, then exponentials
+    float *sm_ = sc + kv_mul * ATT_SUB;      // kv_mul running max
+    float *sl = sm_ + kv_mul;                // kv_mul running sum
+    float *sf = sl + kv_mul;                 // kv_mul rescale factor of this step
     const float rs = sqrtf((float)hs);
-    for (int t = tid; t < T; t += nt) {
-        const float *k = K + (size_t)t * a.kv_dim;
-        for (int j0 = 0; j0 < kv_mul; j0 += 8) {
-            float sacc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int i = 0; i < hs; i += 4) {
-                const float4 kv4 = *(const float4 *)(k + i);
-#pragma unroll
-                for (int jj = 0; jj < 8; jj++) {
-                    if (j0 + jj < kv_mul) { // score += q[i] * k[i] in order (qwen.c:535)
-                        const float *qq = sq + (j0 + jj) * hs + i;
-                        sacc[jj] += qq[0] * kv4.x;
-                        sacc[jj] += qq[1] * kv4.y;
-                        sacc[jj] += qq[2] * kv4.z;
-                        sacc[jj] += qq[3] * kv4.w;
-                    }
-                }
+    for (int i = tid; i < kv_mul * hs; i += nt) sq[i] = a.q[(size_t)kvh * kv_mul * hs + i];
+    if (tid < kv_mul) { sm_[tid] = -INFINITY; sl[tid] = 0.0f; }
+    // each thread owns outputs (j, e) = o, o + nt, ... of the kv_mul * hs accumulators
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int n_out = kv_mul * hs;
+    for (int t0 = t_begin; t0 < t_end; t0 += ATT_SUB) {
+        const int T = min(ATT_SUB, t_end - t0);
+        __syncthreads();
+        const int hs4 = hs / 4;
+        for (int i = tid; i < T * hs4; i += nt) {
+            const int t = i / hs4, c = i - t * hs4;
+            const size_t g = (size_t)(t0 + t) * a.kv_dim + (size_t)kvh * hs + 4 * c;
+            ((float4 *)sk)[i] = *(const float4 *)(a.kc + g);
+            ((float4 *)sv)[i] = *(const float4 *)(a.vc + g);
+        }
+        __syncthreads();
+        for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), i in order
+            const int j = i / T, t = i - j * T;
+            const float *qq = sq + j * hs, *kk = sk + t * hs;
+            float d = 0.0f;
+            for (int e = 0; e < hs; e++) d += qq[e] * kk[e];
+            sc[j * ATT_SUB + t] = d / rs;
+        }
+        __syncthreads();
+        for (int j = wave; j < kv_mul; j += nw) { // online softmax statistics, one wave per head
+            float v = lane < T ? sc[j * ATT_SUB + lane] : -INFINITY;
+            float mx = group_max(v, WAVE);
+            const float m_old = sm_[j], m_new = fmaxf(m_old, mx);
+            const float e = lane < T ? expf(v - m_new) : 0.0f;
+            if (lane < T) sc[j * ATT_SUB + lane] = e;
+            const float sum = wave_sum_from(e, 1);
+            if (lane == 0) {
+                const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                sf[j] = f;
+                sl[j] = sl[j] * f + sum;
+                sm_[j] = m_new;
             }
-            for (int jj = 0; jj < 8 && j0 + jj < kv_mul; jj++) sc[(j0 + jj) * a.chunk + t] = sacc[jj] / rs;
+        }
+        __syncthreads();
+        for (int k = 0; k < 4; k++) {
+            const int o = tid + k * nt;
+            if (o < n_out) {
+                const int j = o / hs, e = o - j * hs;
+                float v = acc[k] * sf[j];
+                for (int t = 0; t < T; t++) v += sc[j * ATT_SUB + t] * sv[t * hs + e];
+                acc[k] = v;
+            }
         }
     }
-    __syncthreads();
-    // softmax statistics per head: one wave per head
-    for (int j = wave; j < kv_mul; j += nw) {
-        float m = -INFINITY;
-        for (int t = lane; t < T; t += WAVE) m = fmaxf(m, sc[j * a.chunk + t]);
-        m = group_max(m, WAVE);
-        float l = 0.0f;
-        for (int t = lane; t < T; t += WAVE) {
-            float e = expf(sc[j * a.chunk + t] - m);
-            sc[j * a.chunk + t] = e;
-            l += e;
-        }
-        l = wave_sum_from(l, 1);
-        if (lane == 0) {
-            float *ml = a.ml + ((size_t)(kvh * kv_mul + j) * a.splits + s) * 2;
-            ml[0] = m;
-            ml[1] = l;
+    for (int k = 0; k < 4; k++) {
+        const int o = tid + k * nt;
+        if (o < n_out) {
+            const int j = o / hs, e = o - j * hs;
+            a.acc[((size_t)(kvh * kv_mul + j) * a.splits + s) * hs + e] = acc[k];
         }
     }
-    __syncthreads();
-    // weighted values: thread (slice, e) sums positions t = slice, slice + slices, ...
-    const int slices = nt / hs;
-    const int sl = tid / hs, e = tid - sl * hs;
-    if (sl < slices) {
-        float acc[16];
-        for (int j = 0; j < 16; j++) acc[j] = 0.0f;
-        for (int t = sl; t < T; t += slices) {
-            const float v = V[(size_t)t * a.kv_dim + e];
-            for (int j = 0; j < kv_mul && j < 16; j++) acc[j] += sc[j * a.chunk + t] * v;
-        }
-        for (int j = 0; j < kv_mul && j < 16; j++) sp[((size_t)sl * kv_mul + j) * hs + e] = acc[j];
-    }
-    __syncthreads();
-    for (int i = tid; i < kv_mul * hs; i += nt) {
-        const int j = i / hs, ee = i - j * hs;
-        float v = 0.0f;
-        for (int k = 0; k < slices; k++) v += sp[((size_t)k * kv_mul + j) * hs + ee];
-        a.acc[((size_t)(kvh * kv_mul + j) * a.splits + s) * hs + ee] = v;
+    if (tid < kv_mul) {
+        float *ml = a.ml + ((size_t)(kvh * kv_mul + tid) * a.splits + s) * 2;
+        ml[0] = sm_[tid];
+        ml[1] = sl[tid];
     }
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv, threads = 256;
-    const int slices = threads / a.hs;
-    const size_t lds = ((size_t)kv_mul * a.hs + (size_t)kv_mul * a.chunk + (size_t)slices * kv_mul * a.hs) * 4;
+    if (kv_mul * a.hs > 4 * threads || a.hs % 4) return hipErrorInvalidValue;
+    const size_t lds = ((size_t)kv_mul * a.hs + 2 * (size_t)ATT_SUB * a.hs + (size_t)kv_mul * ATT_SUB + 3 * kv_mul) * 4;
     hipLaunchKernelGGL(k_attention, dim3(a.n_kv * a.splits), dim3(threads), lds, st, a);
     return hipGetLastError();
 }
@@ -412,13 +511,60 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 // ------------------------------------------------------------------------------------------------------
 // embedding row (qwen.c:498-501, runq.c:490-492) and the step's position/token bookkeeping
 
-__global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
-    __shared__ int tok_s;
+// argmax over the head kernel's per-block partials: larger value wins, equal values keep the lower row
+__device__ __forceinline__ void block_argmax(const float *pv, const int *pi, int np, float *sv, int *si, float *v_out,
+                                             int *i_out) {
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    for (int k = threadIdx.x; k < np; k += blockDim.x) {
+        const float x = pv[k];
+        const int xi = pi[k];
+        if (x > v || (x == v && xi < i)) { v = x; i = xi; }
+    }
+    for (int off = 1; off < WAVE; off <<= 1) {
+        float ov = __shfl_xor(v, off);
+        int oi = __shfl_xor(i, off);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    if (lane == 0) { sv[wave] = v; si[wave] = i; }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        StepCtrl *c = a.ctrl;
-        int pos = c->pos, token = c->token;
-        if (c->mode == 1) {
-            pos = pos + 1;
+        for (int k = 1; k < (int)(blockDim.x / WAVE); k++)
+            if (sv[k] > v || (sv[k] == v && si[k] < i)) { v = sv[k]; i = si[k]; }
+        if (i == 0x7fffffff) i = 0; // every logit NaN: the reference keeps row 0
+        *v_out = v;
+        *i_out = i;
+    }
+}
+
+// Start of a step.  Generate mode: finish the previous step's argmax (qwen.c:591-598, head_ids map
+// qwen.c:683), advance the position and take the prompt token or the argmax (prompt forcing,
+// qwen.c:677-683).  Then the embedding row of the token (qwen.c:498-501, runq.c:490-492).
+__global__ void __launch_bounds__(256) k_step_start(EmbedArgs a) {
+    __shared__ float sv[256 / WAVE];
+    __shared__ int si[256 / WAVE];
+    __shared__ int tok_s;
+    __shared__ float bv;
+    __shared__ int bi, s_mode, s_prev;
+    StepCtrl *c = a.ctrl;
+    // one read of the control block for the whole block, before thread 0 advances it below
+    if (threadIdx.x == 0) {
+        s_mode = c->mode;
+        s_prev = c->pos;
+    }
+    __syncthreads();
+    const int mode = s_mode, prev = s_prev;
+    if (mode == 1 && prev >= 0) block_argmax(a.pv, a.pi, a.np, sv, si, &bv, &bi);
+    if (threadIdx.x == 0) {
+        int pos = prev, token = c->token;
+        if (mode == 1) {
+            if (prev >= 0) {
+                const int next = a.head_ids ? a.head_ids[bi] : bi;
+                c->next_token = next;
+                if (a.gen) a.gen[prev] = next;
+            }
+            pos = prev + 1;
             token = pos < c->n_prompt ? a.prompt[pos] : c->next_token;
             c->pos = pos;
             c->token = token;
@@ -438,34 +584,19 @@ __global__ void __launch_bounds__(256) k_embed(EmbedArgs a) {
 }
 
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_step_start, dim3(1), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 
-// final argmax over the per-block partials (qwen.c:591-598) and the head_ids map (qwen.c:683)
+// final argmax of a step over the head kernel's partials (qwen.c:591-598) and the head_ids map (qwen.c:683)
 __global__ void __launch_bounds__(256) k_argmax(ArgmaxArgs a) {
     __shared__ float sv[256 / WAVE];
     __shared__ int si[256 / WAVE];
-    float v = -INFINITY;
-    int i = 0x7fffffff;
-    for (int k = threadIdx.x; k < a.np; k += blockDim.x) {
-        const float pv = a.pv[k];
-        const int pi = a.pi[k];
-        if (pv > v || (pv == v && pi < i)) { v = pv; i = pi; }
-    }
-    for (int off = 1; off < WAVE; off <<= 1) {
-        float ov = __shfl_xor(v, off);
-        int oi = __shfl_xor(i, off);
-        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-    }
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-    if (lane == 0) { sv[wave] = v; si[wave] = i; }
-    __syncthreads();
+    __shared__ float bv;
+    __shared__ int bi;
+    block_argmax(a.pv, a.pi, a.np, sv, si, &bv, &bi);
     if (threadIdx.x == 0) {
-        for (int k = 1; k < (int)(blockDim.x / WAVE); k++)
-            if (sv[k] > v || (sv[k] == v && si[k] < i)) { v = sv[k]; i = si[k]; }
-        if (i == 0x7fffffff) i = 0; // every logit NaN: the reference keeps row 0
-        const int next = a.head_ids ? a.head_ids[i] : i;
+        const int next = a.head_ids ? a.head_ids[bi] : bi;
         a.ctrl->next_token = next;
         if (a.gen) a.gen[a.ctrl->pos] = next;
     }

@@ -29,7 +29,6 @@
 
 namespace {
 
-constexpr int ATT_CHUNK = 256;
 
 struct Layer {
     TiledMat qkv, o, gu, down;
@@ -113,8 +112,19 @@ double attn_bytes(const llm_model *m, int pos) { // K and V rows read, q read, p
     return 2.0 * (pos + 1) * m->kv_dim * 4.0 + m->info.dim * 4.0 + m->info.n_heads * 4.0 * (m->hs + 2);
 }
 
+hipError_t launch_finalize(llm_model *m) {
+    ArgmaxArgs g;
+    g.pv = m->part_v;
+    g.pi = m->part_i;
+    g.np = m->s_head.grid;
+    g.head_ids = m->head_ids_d;
+    g.ctrl = m->ctrl;
+    g.gen = m->gen;
+    return launch_argmax(g, m->st);
+}
+
 // Enqueue one decode step on m->st.  prof != NULL records events around every launch.
-int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint) {
+int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finalize) {
     const llm_info &I = m->info;
     const int dim = I.dim, kv = m->kv_dim;
     auto mark = [&](int kind, double bytes) {
@@ -145,6 +155,11 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint) {
     e.ctrl = m->ctrl;
     e.prompt = m->prompt;
     e.tokens = m->tokens;
+    e.pv = m->part_v;
+    e.pi = m->part_i;
+    e.np = m->s_head.grid;
+    e.head_ids = m->head_ids_d;
+    e.gen = m->gen;
     mark(K_EMBED, dim + dim / m->gs * (m->emb_sf32 ? 4.0 : 2.0) + dim * 4.0);
     HIP_OR_FAIL("llm", launch_embed(e, m->st));
     done();
@@ -184,7 +199,6 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint) {
         t.n_kv = I.n_kv_heads;
         t.hs = m->hs;
         t.kv_dim = kv;
-        t.chunk = ATT_CHUNK;
         t.splits = m->att_splits;
         t.ctrl = m->ctrl;
         mark(K_ATTN, attn_bytes(m, pos_hint));
@@ -197,7 +211,6 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint) {
         a.n_heads = I.n_heads;
         a.head_size = m->hs;
         a.att_splits = m->att_splits;
-        a.att_chunk = ATT_CHUNK;
         a.out = m->x;
         mark(K_O, gemv_algo_bytes(dim, dim, wb, m->gs, sf));
         HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_ATTN, EPI_RESID, a, Ly.s_o.grid, m->st));
@@ -233,23 +246,18 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint) {
     HIP_OR_FAIL("llm", launch_gemv(8, m->gs, m->head.sf32, PRO_NORM, EPI_ARGMAX, a, m->s_head.grid, m->st));
     done();
 
-    ArgmaxArgs g;
-    g.pv = m->part_v;
-    g.pi = m->part_i;
-    g.np = m->s_head.grid;
-    g.head_ids = m->head_ids_d;
-    g.ctrl = m->ctrl;
-    g.gen = m->gen;
-    mark(K_ARGMAX, m->s_head.grid * 8.0);
-    HIP_OR_FAIL("llm", launch_argmax(g, m->st));
-    done();
+    if (finalize) { // the step's own argmax; in a captured sequence the next step's start kernel does it
+        mark(K_ARGMAX, m->s_head.grid * 8.0);
+        HIP_OR_FAIL("llm", launch_finalize(m));
+        done();
+    }
     return 0;
 }
 
 int capture(llm_model *m, bool hist, hipGraphExec_t *out) {
     hipGraph_t g;
     HIP_OR_FAIL("llm", hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(m, hist, nullptr, 0);
+    int rc = enqueue_step(m, hist, nullptr, 0, false);
     hipError_t e = hipStreamEndCapture(m->st, &g);
     if (rc || e != hipSuccess) {
         fprintf(stderr, "llm: graph capture failed: %s\n", hipGetErrorString(e));
@@ -352,7 +360,9 @@ int finish_setup(llm_model *m) {
         ly.s_down = gemv_pick_shape(ly.down, PRO_XQ, EPI_RESID, ord);
     }
     m->s_head = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, m->kind == 1);
-    m->att_splits = (m->ctx + ATT_CHUNK - 1) / ATT_CHUNK;
+    // attention slices: up to 64 per kv head, each at least ATT_SUB positions
+    m->att_splits = (m->ctx + ATT_SUB - 1) / ATT_SUB;
+    if (m->att_splits > 64) m->att_splits = 64;
     const size_t kvn = (size_t)I.n_layers * m->ctx * m->kv_dim;
     if (dalloc(m, &m->kc, kvn * 4) || dalloc(m, &m->vc, kvn * 4) || dalloc(m, &m->x, (size_t)I.dim * 4) ||
         dalloc(m, &m->q, (size_t)I.dim * 4) ||
@@ -472,9 +482,9 @@ int load_qwb(llm_model *m, const char *path, int ctx) {
     size_t total = 0;
     for (Layer &ly : m->L) {
         ly.qkv = tiled_describe(dim + 2 * kv, dim, 32, 4, 0, 16);
-        ly.o = tiled_describe(dim, dim, 32, 4, 0, 16);
+        ly.o = tiled_describe(dim, dim, 32, 4, 0, gemv_row_block(dim, dim));
         ly.gu = tiled_describe(2 * hid, dim, 32, 4, 0, 16);
-        ly.down = tiled_describe(dim, hid, 32, 4, 0, 16);
+        ly.down = tiled_describe(dim, hid, 32, 4, 0, gemv_row_block(dim, hid));
         total += round256(ly.qkv.bytes) + round256(ly.o.bytes) + round256(ly.gu.bytes) + round256(ly.down.bytes);
     }
     m->head = tiled_describe(I.n_logits, dim, 32, 8, 0, 16);
@@ -762,7 +772,7 @@ extern "C" int llm_forward(llm_model *m, int token, int pos, float *logits) {
     }
     hipSetDevice(m->device);
     if (set_ctrl(m, pos, token, 0, 0)) return -1;
-    if (enqueue_step(m, false, nullptr, pos)) return -1;
+    if (enqueue_step(m, false, nullptr, pos, true)) return -1;
     if (logits)
         HIP_OR_FAIL("llm_forward", hipMemcpyAsync(logits, m->logits, (size_t)m->info.n_logits * 4,
                                                   hipMemcpyDeviceToHost, m->st));
@@ -819,6 +829,7 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
         const int upto = ran + batch < last_pos ? ran + batch : last_pos;
         for (int p = ran + 1; p <= upto; p++) HIP_OR_FAIL("llm_generate", hipGraphLaunch(*g, m->st));
         ran = upto > ran ? upto : ran;
+        HIP_OR_FAIL("llm_generate", launch_finalize(m)); // argmax of the batch's last step
         HIP_OR_FAIL("llm_generate", hipMemcpyAsync(gen.data() + checked, m->gen + checked,
                                                    (size_t)(ran - checked + 1) * 4, hipMemcpyDeviceToHost, m->st));
         HIP_OR_FAIL("llm_generate", hipStreamSynchronize(m->st));
@@ -895,7 +906,7 @@ extern "C" int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int 
         pr.used = 0;
         pr.kind.clear();
         pr.bytes.clear();
-        if (enqueue_step(m, false, &pr, c.pos + 1 + s)) return -1;
+        if (enqueue_step(m, false, &pr, c.pos + 1 + s, false)) return -1;
         HIP_OR_FAIL("llm_profile", hipStreamSynchronize(m->st));
         for (size_t i = 0; i < pr.kind.size(); i++) {
             float t = 0;
