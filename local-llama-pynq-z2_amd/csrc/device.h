@@ -45,12 +45,55 @@ __device__ __forceinline__ float group_max(float v, int width) { // max over ali
     return v;
 }
 
-// Deterministic block-wide sum (fixed order: lanes in a butterfly, then waves in index order).
-// `scratch` needs one float per wave.  Every thread gets the result.
+// Value of another lane of the same row of 16 lanes through a DPP operand (no LDS round trip).  CTRL is
+// the gfx9 DPP control: 0xB1 = lane ^ 1, 0x4E = lane ^ 2 (quad permutes), 0x141 = 7 - lane within each 8
+// (half-row mirror), 0x140 = 15 - lane within the row (row mirror).  Call with the whole wave active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Max over aligned groups of 8 (or 16) lanes.  Max is exact, so the mirrors pair lanes as well as a
+// butterfly would: after the quad steps every lane holds its quad's max, and lane i with lane 7 - i (15 - i)
+// joins two quads (two eights).
+__device__ __forceinline__ float max8(float m) {
+    m = fmaxf(m, dpp_get<0xB1>(m));
+    m = fmaxf(m, dpp_get<0x4E>(m));
+    return fmaxf(m, dpp_get<0x141>(m));
+}
+__device__ __forceinline__ float max16(float m) {
+    m = max8(m);
+    return fmaxf(m, dpp_get<0x140>(m));
+}
+// Max over the whole wave (every lane gets it).
+__device__ __forceinline__ float wave_max(float m) {
+    m = max16(m);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Sum of a whole wave in a fixed order: pairs, quads, eights and rows of 16 by DPP, then the four row sums
+// as (row0 + row1) + (row2 + row3).  Every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_get<0xB1>(v);
+    v += dpp_get<0x4E>(v);
+    v += dpp_get<0x141>(v);
+    v += dpp_get<0x140>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// Deterministic block-wide sum (fixed order: wave_sum, then waves in index order).  `scratch` needs one
+// float per wave and must not be read by anyone else at the time of the call.  Every thread gets the result.
 __device__ __forceinline__ float block_sum(float v, float *scratch) {
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE, nw = blockDim.x / WAVE;
-    v = wave_sum_from(v, 1);
-    __syncthreads();
+    v = wave_sum(v);
     if (lane == 0) scratch[w] = v;
     __syncthreads();
     float t = 0.0f;
@@ -58,20 +101,25 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
     return t;
 }
 
-// Quantize n floats held in LDS (`v`) into int8 `q` and fp32 scales `s` (LDS or global), groups of gs
-// (32 or 64), by the whole block: a group of gs lanes per group, max by butterfly (exact in any order).
+// Quantize n floats held in LDS (`v`, 16-byte aligned) into int8 `q` (4-byte aligned) and fp32 scales `s`
+// (LDS or global), groups of gs (32 or 64; n a multiple of gs), by the whole block.  Each lane takes 4
+// consecutive values, so a group is gs/4 = 8 or 16 lanes of one DPP row and its max is max8 / max16.
 __device__ __forceinline__ void block_quantize(const float *v, int n, int gs, int flavor, int8_t *q, float *s) {
-    const int gpp = blockDim.x / gs; // groups per pass
-    const int ng = n / gs;
-    const int my = threadIdx.x / gs, e = threadIdx.x % gs;
-    for (int g0 = 0; g0 < ng; g0 += gpp) {
-        const int g = g0 + my;
-        float x = (my < gpp && g < ng) ? v[g * gs + e] : 0.0f;
-        float m = group_max(fabsf(x), gs);
-        if (my < gpp && g < ng) {
-            float scale = quant_scale(m, flavor), inv = quant_inv(scale);
-            q[g * gs + e] = quant_one(x, scale, inv, flavor);
-            if (e == 0) s[g] = scale;
+    const int nq = n / 4, lpg = gs / 4;
+    for (int i0 = 0; i0 < nq; i0 += blockDim.x) {
+        const int i = i0 + threadIdx.x;
+        const bool ok = i < nq; // whole groups are in or out: nq is a multiple of lpg
+        const float4 x = ((const float4 *)v)[ok ? i : 0];
+        float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+        m = gs == 64 ? max16(m) : max8(m);
+        if (ok) {
+            const float scale = quant_scale(m, flavor), inv = quant_inv(scale);
+            const uint32_t b0 = (uint8_t)quant_one(x.x, scale, inv, flavor);
+            const uint32_t b1 = (uint8_t)quant_one(x.y, scale, inv, flavor);
+            const uint32_t b2 = (uint8_t)quant_one(x.z, scale, inv, flavor);
+            const uint32_t b3 = (uint8_t)quant_one(x.w, scale, inv, flavor);
+            ((uint32_t *)q)[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if ((i & (lpg - 1)) == 0) s[i / lpg] = scale;
         }
     }
 }

@@ -36,6 +36,8 @@ struct State {
     size_t total = 0;
     char last_err[256] = "";
     uint8_t *stage = nullptr;    // int rowmap for repacks
+    int8_t *xstage = nullptr;    // activations whose device address is not 16-byte aligned (the kernel reads
+                                 // them as 16-byte vectors)
     int *rowmap = nullptr;
     size_t rowmap_n = 0;
 };
@@ -115,14 +117,19 @@ int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out
         fprintf(stderr, "%s: xq, xs or out range is not inside a buffer from fpga_alloc()\n", who);
         return -1;
     }
-    HIP_OR_FAIL(who, hipMemcpyAsync((void *)xq, host_of(bx, xq), (size_t)n, hipMemcpyHostToDevice, S.st));
+    int8_t *xdev = (int8_t *)xq;
+    if (xq & 15) {
+        if (!S.xstage) HIP_OR_FAIL(who, hipMalloc(&S.xstage, MATVEC_HIP_MAX_N));
+        xdev = S.xstage;
+    }
+    HIP_OR_FAIL(who, hipMemcpyAsync(xdev, host_of(bx, xq), (size_t)n, hipMemcpyHostToDevice, S.st));
     HIP_OR_FAIL(who, hipMemcpyAsync((void *)xs, host_of(bxs, xs), (size_t)(n / gs) * 4, hipMemcpyHostToDevice, S.st));
     GemvArgs a;
     memset(&a, 0, sizeof a);
     a.W = W->T;
     a.kw = W->shape.kw;
     a.nb = W->shape.nb;
-    a.xq = (const int8_t *)xq;
+    a.xq = xdev;
     a.xs = (const float *)xs;
     a.out = (float *)out;
     HIP_OR_FAIL(who, launch_gemv(W->T.wbits, W->T.gs, W->T.sf32, PRO_XQ, EPI_STORE, a, W->shape.grid, S.st));
@@ -258,6 +265,8 @@ extern "C" void fpga_close(void) {
     if (S.rowmap) hipFree(S.rowmap);
     S.rowmap = nullptr;
     S.rowmap_n = 0;
+    if (S.xstage) hipFree(S.xstage);
+    S.xstage = nullptr;
     if (S.st) hipStreamDestroy(S.st);
     S.st = nullptr;
     S.total = 0;

@@ -8,6 +8,12 @@
 #include "device.h"
 #include "kernels.h"
 
+// Phase hooks for timing studies: a harness that includes this file may define KERNEL_MARK(k) to record
+// a timestamp of phase k; the library's own build compiles them away.
+#ifndef KERNEL_MARK
+#define KERNEL_MARK(k)
+#endif
+
 #include <math.h>
 
 // ------------------------------------------------------------------------------------------------------
@@ -78,16 +84,16 @@ __device__ __forceinline__ void load_batch(const uint8_t *base, size_t rec_bytes
                                            uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
                                            uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
     using F = Fmt<WB, GSZ, SF32>;
+    // Every load is issued: a chunk index past the end reads the row-block's last record, which use_batch
+    // then skips.  Unconditional loads keep the wave from waiting for them at a branch merge.
 #pragma unroll
     for (int u = 0; u < F::UNROLL; u++) {
-        const int c = c0 + u * kw;
-        if (c < nchunks) {
-            const uint8_t *rec = base + (size_t)c * rec_bytes;
+        const int c = min(c0 + u * kw, nchunks - 1);
+        const uint8_t *rec = base + (size_t)c * rec_bytes;
 #pragma unroll
-            for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
-            if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
-            else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
-        }
+        for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
+        if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
+        else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
     }
 }
 
@@ -123,17 +129,46 @@ __device__ __forceinline__ void qkv_neox_row(int R, int hs, int *e, int *ep, int
     *ep = hh * hs + (r < 8 ? half + *i : *i);
 }
 
+// Smallest power of two >= s (s in 1..64): the lanes that one head's attention slices take in the merge.
+__device__ __forceinline__ int pow2_at_least(int s) {
+    int w = 1;
+    while (w < s) w <<= 1;
+    return w;
+}
+
+// Merge weights of the attention slices of head h (SW lanes per head, lane k holds slice k's (max, sum)):
+// exp(m_k - m) / sum_j l_j exp(m_j - m), m the largest slice maximum (the softmax of qwen.c:346-352 taken
+// over the slices).
+__device__ __forceinline__ void merge_weights(float2 st, int h, int k, int S, int SW, int nh, float *wgt) {
+    const bool ok = h < nh && k < S;
+    const float mk = ok ? st.x : -INFINITY;
+    const float m = group_max(mk, SW);
+    const float f = ok ? expf(mk - m) : 0.0f;
+    float l = ok ? st.y * f : 0.0f;
+    for (int off = 1; off < SW; off <<= 1) l += __shfl_xor(l, off);
+    if (ok) wgt[h * S + k] = f * (1.0f / l);
+}
+
+// 16 bytes as a native vector: copied as a register value (a struct copy would go through memory)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Vectors of 16 bytes per thread that a prologue loads in its first pass, before the weights.
+#define PRO_VEC 4
+// Slices of attention partials one merge pass loads per thread.
+#define MERGE_KB 8
+
 template <int WB, int GSZ, int SF32, int PRO, int EPI>
 __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     using F = Fmt<WB, GSZ, SF32>;
     extern __shared__ __align__(16) uint8_t lds[];
     const TiledMat &W = a.W;
-    const int rb = W.rb, gpc = WAVE / rb, ngp = W.nchunks * gpc;
-    const int tid = threadIdx.x, nt = blockDim.x, wave = tid / WAVE, lane = tid & (WAVE - 1), nw = nt / WAVE;
+    const int rb = W.rb, gpc = WAVE / rb, ngp = W.nchunks * gpc, ngp4 = (ngp + 3) & ~3;
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & (WAVE - 1), nw = nt / WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE); // uniform: wave-level branches stay scalar
     const int n = W.n;
     int8_t *sxq = (int8_t *)lds;                          // ngp * GSZ
-    float *sxs = (float *)(lds + (size_t)ngp * GSZ);      // ngp
-    float *sred = sxs + ngp;                              // nw * 64
+    float *sxs = (float *)(lds + (size_t)ngp * GSZ);      // ngp4
+    float *sred = sxs + ngp4;                             // nw * 64
     float *srow = sred + nw * WAVE;                       // nb * rb
     float *sv = srow + a.nb * rb;                         // prologue / epilogue floats
     const int my_nb = wave / a.kw, my_kw = wave - my_nb * a.kw;
@@ -141,100 +176,175 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     const int n_it = (W.nblocks + a.nb - 1) / a.nb;
     const int g_lane = lane / rb;
     const int it0 = blockIdx.x;
-
-    // (1) weights of this block's first iteration: the first batch is issued before anything else
-    uint4 wa[F::UNROLL][F::PIECES], wb[F::UNROLL][F::PIECES];
-    uint32_t sa[F::UNROLL], sb[F::UNROLL];
-    {
-        const int b = it0 * a.nb + my_nb;
-        if (it0 < n_it && b < W.nblocks)
-            load_batch<WB, GSZ, SF32>(W.data + (size_t)b * W.nchunks * W.rec, W.rec, W.nchunks, my_kw, a.kw, lane, wa, sa);
-    }
-    // (2) the step's position and the epilogue operands of this thread's first row
+    KERNEL_MARK(0);
     const bool need_pos = PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX;
     const int pos = need_pos ? a.ctrl->pos : 0;
+
+    // (1) the prologue's operands for its first pass, issued first: loads complete in issue order, so
+    // waiting for these does not also wait for the weights issued after them.  Indices past the end are
+    // clamped (the values are loaded and never used).
+    u32x4 px[PRO_VEC];      // PRO_XQ: 16 int8 activations each
+    float pxs[2];           // PRO_XQ: group scales
+    float4 pn[PRO_VEC], pg[PRO_VEC]; // PRO_NORM: x and gains
+    float2 pst = make_float2(0.0f, 0.0f); // PRO_ATTN: (max, sum) of one (head, slice)
+    float4 pab[MERGE_KB];   // PRO_ATTN: value sums of the first slot's first slices
+    int S = 1, SW = 1;      // PRO_ATTN: slices of this step, lanes per head in the statistics
+    if constexpr (PRO == PRO_XQ) {
+        const u32x4 *src = (const u32x4 *)a.xq;
+        const int nq = n / 16;
+#pragma unroll
+        for (int k = 0; k < PRO_VEC; k++) px[k] = src[min(tid + k * nt, nq - 1)];
+#pragma unroll
+        for (int k = 0; k < 2; k++) pxs[k] = a.xs[min(tid + k * nt, W.ng - 1)];
+    } else if constexpr (PRO == PRO_NORM) {
+        const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.norm_w;
+        const int nv = n / 4;
+#pragma unroll
+        for (int k = 0; k < PRO_VEC; k++) {
+            const int i = min(tid + k * nt, nv - 1);
+            pn[k] = x4[i];
+            pg[k] = w4[i];
+        }
+    } else if constexpr (PRO == PRO_ATTN) {
+        const int hs = a.head_size, SP = a.att_splits, nh = a.n_heads;
+        int chunk;
+        att_slices(pos, SP, &S, &chunk);
+        SW = pow2_at_least(S);
+        const int h = wave * (WAVE / SW) + lane / SW, k = lane & (SW - 1);
+        pst = ((const float2 *)a.att_ml)[(size_t)min(h, nh - 1) * SP + min(k, S - 1)];
+        const int v = min(tid, n / 4 - 1), hh = 4 * v / hs, e = 4 * v - hh * hs;
+#pragma unroll
+        for (int kk = 0; kk < MERGE_KB; kk++)
+            pab[kk] = *(const float4 *)(a.att_acc + ((size_t)hh * SP + min(kk, S - 1)) * hs + e);
+    }
+
+    asm volatile("" ::: "memory"); // keep the issue order: prologue operands, then weights
+
+    // (2) weights of this block's first iteration
+    uint4 wa[F::UNROLL][F::PIECES], wb[F::UNROLL][F::PIECES];
+    uint32_t sa[F::UNROLL], sb[F::UNROLL];
+    load_batch<WB, GSZ, SF32>(W.data + (size_t)min(it0 * a.nb + my_nb, W.nblocks - 1) * W.nchunks * W.rec, W.rec,
+                              W.nchunks, my_kw, a.kw, lane, wa, sa);
+
+    // (3) the epilogue operands of this thread's first row (clamped row index, used only for valid rows)
     float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f, pre_x = 0.0f;
     {
-        const int R = it0 * rows_it + tid;
-        if (tid < rows_it && R < W.rows) {
-            if constexpr (EPI == EPI_RESID) pre_x = a.out[R];
-            if constexpr (EPI == EPI_QKV) {
-                const int half = a.head_size / 2;
-                if (a.rope_kind == ROPE_NEOX) {
-                    if (R < a.dim + a.kv_dim) {
-                        int e, ep, i;
-                        bool first;
-                        qkv_neox_row(R, a.head_size, &e, &ep, &i, &first);
-                        pre_b = a.bias[e];
-                        pre_bp = a.bias[ep];
-                        pre_c = a.rope_cos[(size_t)pos * half + i];
-                        pre_s = a.rope_sin[(size_t)pos * half + i];
-                    } else {
-                        pre_b = a.bias[R];
-                    }
-                } else if (R < a.dim + a.kv_dim) {
-                    const int e = R < a.dim ? R : R - a.dim, i = (e % a.head_size) / 2;
-                    pre_c = a.rope_cos[(size_t)pos * half + i];
-                    pre_s = a.rope_sin[(size_t)pos * half + i];
-                }
+        const int R = min(it0 * rows_it + tid, W.rows - 1);
+        if constexpr (EPI == EPI_RESID) pre_x = a.out[R];
+        if constexpr (EPI == EPI_QKV) {
+            const int half = a.head_size / 2, rot = a.dim + a.kv_dim, Rr = min(R, rot - 1);
+            int i;
+            if (a.rope_kind == ROPE_NEOX) {
+                int e, ep;
+                bool first;
+                qkv_neox_row(Rr, a.head_size, &e, &ep, &i, &first);
+                pre_b = a.bias[R < rot ? e : R];
+                pre_bp = a.bias[R < rot ? ep : R];
+            } else {
+                const int e = Rr < a.dim ? Rr : Rr - a.dim;
+                i = (e % a.head_size) / 2;
             }
+            pre_c = a.rope_cos[(size_t)pos * half + i];
+            pre_s = a.rope_sin[(size_t)pos * half + i];
         }
     }
 
-    // (3) prologue: int8 activations and their scales into LDS
+    // (4) prologue: int8 activations and their scales into LDS
     if constexpr (PRO == PRO_XQ) {
-        const uint32_t *src = (const uint32_t *)a.xq;
-        uint32_t *dst = (uint32_t *)sxq;
-        for (int i = tid; i < ngp * GSZ / 4; i += nt) dst[i] = i < n / 4 ? src[i] : 0u;
-        for (int i = tid; i < ngp; i += nt) sxs[i] = i < W.ng ? a.xs[i] : 0.0f;
+        const int nq = n / 16;
+        u32x4 *dst = (u32x4 *)sxq;
+        // stores at the clamped index too: a thread past the end writes the last vector's own value again
+        // (an unconditional use keeps the compiler from moving the loads down to here)
+#pragma unroll
+        for (int k = 0; k < PRO_VEC; k++) dst[min(tid + k * nt, nq - 1)] = px[k];
+        for (int i = PRO_VEC * nt + tid; i < nq; i += nt) dst[i] = ((const u32x4 *)a.xq)[i];
+#pragma unroll
+        for (int k = 0; k < 2; k++) sxs[min(tid + k * nt, W.ng - 1)] = pxs[k];
+        for (int i = 2 * nt + tid; i < W.ng; i += nt) sxs[i] = a.xs[i];
     } else {
+        float4 *sv4 = (float4 *)sv;
         if constexpr (PRO == PRO_NORM) {
             // rmsnorm (qwen.c:337-344, runq.c:394-407): ss = sum x^2; ss /= n; ss += eps; ss = 1/sqrtf(ss)
-            // x and the gains are read in one pass (gains parked in the upper half of sv)
+            const int nv = n / 4;
             float part = 0.0f;
-            for (int i = tid; i < n; i += nt) {
-                const float v = a.x[i], w = a.norm_w[i];
-                sv[i] = v;
-                sv[n + i] = w;
-                part += v * v;
+#pragma unroll
+            for (int k = 0; k < PRO_VEC; k++)
+                if (tid + k * nt < nv) {
+                    const float4 v = pn[k];
+                    part += v.x * v.x;
+                    part += v.y * v.y;
+                    part += v.z * v.z;
+                    part += v.w * v.w;
+                }
+            // vectors beyond the first pass are parked in LDS (x in sv, gains in the n floats after it)
+            for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
+                const float4 v = ((const float4 *)a.x)[i], g = ((const float4 *)a.norm_w)[i];
+                sv4[i] = v;
+                sv4[nv + i] = g;
+                part += v.x * v.x;
+                part += v.y * v.y;
+                part += v.z * v.z;
+                part += v.w * v.w;
             }
             float ss = block_sum(part, sred);
             ss /= (float)n;
             ss += a.eps;
             ss = 1.0f / sqrtf(ss);
-            for (int i = tid; i < n; i += nt) sv[i] = sv[n + i] * (ss * sv[i]);
-        } else { // PRO_ATTN: merge the attention slices of every head (weights in LDS), then xb = acc / l
-            const int hs = a.head_size, SP = a.att_splits, nh = a.n_heads;
-            int S, chunk;
-            att_slices(pos, SP, &S, &chunk);
-            float *wgt = sv + n; // nh * S merge weights
-            for (int h = tid; h < nh; h += nt) {
-                const float *ml = a.att_ml + (size_t)h * SP * 2;
-                float m = ml[0];
-                for (int k = 1; k < S; k++) m = fmaxf(m, ml[2 * k]);
-                float l = 0.0f;
-                for (int k = 0; k < S; k++) {
-                    const float f = expf(ml[2 * k] - m);
-                    wgt[h * S + k] = f;
-                    l += ml[2 * k + 1] * f;
+#pragma unroll
+            for (int k = 0; k < PRO_VEC; k++)
+                if (tid + k * nt < nv) {
+                    const float4 v = pn[k], g = pg[k];
+                    sv4[tid + k * nt] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
                 }
-                const float inv = 1.0f / l;
-                for (int k = 0; k < S; k++) wgt[h * S + k] *= inv;
+            for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
+                const float4 v = sv4[i], g = sv4[nv + i];
+                sv4[i] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
+            }
+        } else { // PRO_ATTN: merge the attention slices of every head, then xb = acc / l
+            // statistics: SW lanes per head, lane k holds slice k
+            const int hs = a.head_size, SP = a.att_splits, nh = a.n_heads, hpp = nw * (WAVE / SW);
+            float *wgt = sv + n; // nh * S
+            const int k = lane & (SW - 1), h_lane = wave * (WAVE / SW) + lane / SW;
+            merge_weights(pst, h_lane, k, S, SW, nh, wgt);
+            for (int h0 = hpp; h0 < nh; h0 += hpp) {
+                const int h = h0 + h_lane;
+                merge_weights(((const float2 *)a.att_ml)[(size_t)min(h, nh - 1) * SP + min(k, S - 1)], h, k, S, SW,
+                              nh, wgt);
             }
             __syncthreads();
-            for (int i = tid; i < n; i += nt) {
-                const int h = i / hs, e = i - h * hs;
-                float v = 0.0f;
-                for (int k = 0; k < S; k++) v += a.att_acc[((size_t)h * SP + k) * hs + e] * wgt[h * S + k];
-                sv[i] = v;
+            // value slots of 4 elements: sum over slices in slice order
+            const int nv = n / 4;
+            for (int v0 = 0; v0 < nv; v0 += nt) {
+                const int v = min(v0 + tid, nv - 1), hh = 4 * v / hs, e = 4 * v - hh * hs;
+                float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                for (int k0 = 0; k0 < S; k0 += MERGE_KB) {
+                    if (v0 != 0 || k0 != 0) {
+#pragma unroll
+                        for (int kk = 0; kk < MERGE_KB; kk++)
+                            pab[kk] = *(const float4 *)(a.att_acc + ((size_t)hh * SP + min(k0 + kk, S - 1)) * hs + e);
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < MERGE_KB; kk++)
+                        if (k0 + kk < S) {
+                            const float w = wgt[hh * S + k0 + kk];
+                            acc.x += pab[kk].x * w;
+                            acc.y += pab[kk].y * w;
+                            acc.z += pab[kk].z * w;
+                            acc.w += pab[kk].w * w;
+                        }
+                }
+                if (v0 + tid < nv) sv4[v0 + tid] = acc;
             }
         }
         __syncthreads();
         block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
         for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
-        for (int i = W.ng + tid; i < ngp; i += nt) sxs[i] = 0.0f;
     }
+    for (int i = W.ng + tid; i < ngp; i += nt) sxs[i] = 0.0f;
+    if constexpr (PRO == PRO_XQ)
+        for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
     __syncthreads();
+    KERNEL_MARK(1);
 
     // (4) main loop over iterations (usually one per block), batches double-buffered
     float best_v = -INFINITY;
@@ -256,6 +366,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
                 if (c0 + 2 * step >= W.nchunks) break;
             }
         }
+        KERNEL_MARK(2);
         acc = wave_sum_from(acc, rb); // lanes holding the same row
         if (lane < rb) sred[wave * rb + lane] = acc;
         __syncthreads();
@@ -369,16 +480,16 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             a.part_idx[blockIdx.x] = i;
         }
     }
+    KERNEL_MARK(3);
 }
 
 size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
     const TiledMat &W = a.W;
-    const int ngp = W.nchunks * (WAVE / W.rb);
-    size_t b = (size_t)ngp * W.gs + (size_t)ngp * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
+    const int ngp = W.nchunks * (WAVE / W.rb), ngp4 = (ngp + 3) & ~3;
+    size_t b = (size_t)ngp * W.gs + (size_t)ngp4 * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
     size_t extra = 0;
     if (pro == PRO_NORM) extra = (size_t)W.n * 8;
-    if (pro == PRO_ATTN) extra = (size_t)W.n * 4;
-    if (pro == PRO_ATTN) extra += (size_t)a.n_heads * a.att_splits * 4;
+    if (pro == PRO_ATTN) extra = (size_t)W.n * 4 + (size_t)a.n_heads * a.att_splits * 4;
     if (epi == EPI_SWIGLU) extra = extra > (size_t)a.nb * W.rb * 2 ? extra : (size_t)a.nb * W.rb * 2;
     return b + extra + 16;
 }
@@ -405,6 +516,12 @@ static hipError_t launch_fmt(int pro, int epi, const GemvArgs &a, int grid, hipS
 }
 
 hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &a, int grid, hipStream_t st) {
+    // the prologues read their inputs as 16-byte vectors (8 bytes for the attention statistics)
+    auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
+    if (a.W.n % 32 || (pro == PRO_XQ && !al(a.xq, 16)) || (pro == PRO_NORM && (!al(a.x, 16) || !al(a.norm_w, 16))) ||
+        (pro == PRO_ATTN && (!al(a.att_acc, 16) || !al(a.att_ml, 8) || a.head_size % 4 || a.att_splits < 1 ||
+                             a.att_splits > 64)))
+        return hipErrorInvalidValue;
     if (wbits == 4 && gs == 32 && !sf32) return launch_fmt<4, 32, 0>(pro, epi, a, grid, st);
     if (wbits == 8 && gs == 32 && !sf32) return launch_fmt<8, 32, 0>(pro, epi, a, grid, st);
     if (wbits == 8 && gs == 32 && sf32) return launch_fmt<8, 32, 1>(pro, epi, a, grid, st);
@@ -419,6 +536,10 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
 // slice's running max, sum of exponentials and exp-weighted value sum (online softmax), which the
 // o-projection's prologue merges.  Scores are sequential dot products in the reference's order.
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vectors per thread for one sub-chunk of K (and as many of V): ATT_SUB * hs / 4 <= ATT_VEC * 256
+#define ATT_VEC 4
+
 __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
     const int pos = a.ctrl->pos;
@@ -426,36 +547,66 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
     int S, chunk;
     att_slices(pos, a.splits, &S, &chunk);
     if (s >= S) return;
+    KERNEL_MARK(0);
     const int t_begin = s * chunk, t_end = min(t_begin + chunk, pos + 1);
-    const int hs = a.hs, kv_mul = a.n_heads / a.n_kv, tid = threadIdx.x, nt = blockDim.x;
-    const int wave = tid / WAVE, lane = tid & (WAVE - 1), nw = nt / WAVE;
+    const int hs = a.hs, hs4 = hs / 4, kv_mul = a.n_heads / a.n_kv, tid = threadIdx.x, nt = blockDim.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid & (WAVE - 1), nw = nt / WAVE;
+    // K rows are padded to hs + 4 floats: the score loop's lanes read different rows at the same column,
+    // which an unpadded power-of-two stride would put in one LDS bank
+    const int ks = hs + 4;
     float *sq = sm;                          // kv_mul * hs
-    float *sk = sq + kv_mul * hs;            // ATT_SUB * hs
-    float *sv = sk + ATT_SUB * hs;           // ATT_SUB * hs
+    float *sk = sq + kv_mul * hs;            // ATT_SUB * ks
+    float *sv = sk + ATT_SUB * ks;           // ATT_SUB * hs
     float *sc = sv + ATT_SUB * hs;           // kv_mul * ATT_SUB scores, then exponentials
     float *sm_ = sc + kv_mul * ATT_SUB;      // kv_mul running max
     float *sl = sm_ + kv_mul;                // kv_mul running sum
     float *sf = sl + kv_mul;                 // kv_mul rescale factor of this step
     const float rs = sqrtf((float)hs);
-    for (int i = tid; i < kv_mul * hs; i += nt) sq[i] = a.q[(size_t)kvh * kv_mul * hs + i];
+
+    // Every global load of a sub-chunk is issued before the first is waited for: q of the kv_mul heads with
+    // the first sub-chunk, each later sub-chunk while the previous one is computed.  Vector indices past
+    // the end are clamped; their stores write the last vector's own value again.
+    const int nq4 = kv_mul * hs4; // <= nt
+    const f32x4 rq = ((const f32x4 *)(a.q + (size_t)kvh * kv_mul * hs))[min(tid, nq4 - 1)];
+    f32x4 rk[ATT_VEC], rv[ATT_VEC];
+    // vector k of this thread in a sub-chunk: row t, column vector c (clamped to the sub-chunk's last)
+    auto kv_index = [&](int t0, int k, int *t, int *c) {
+        const int cnt = min(ATT_SUB, t_end - t0) * hs4, i = min(tid + k * nt, cnt - 1);
+        *t = i / hs4;
+        *c = i - *t * hs4;
+    };
+    auto load_kv = [&](int t0) {
+#pragma unroll
+        for (int k = 0; k < ATT_VEC; k++) {
+            int t, c;
+            kv_index(t0, k, &t, &c);
+            const size_t gi = (size_t)(t0 + t) * a.kv_dim + (size_t)kvh * hs + 4 * c;
+            rk[k] = *(const f32x4 *)(a.kc + gi);
+            rv[k] = *(const f32x4 *)(a.vc + gi);
+        }
+    };
+    load_kv(t_begin);
+    asm volatile("" ::: "memory"); // every load above is issued before the first store waits for one
+    ((f32x4 *)sq)[min(tid, nq4 - 1)] = rq;
     if (tid < kv_mul) { sm_[tid] = -INFINITY; sl[tid] = 0.0f; }
     // each thread owns outputs (j, e) = o, o + nt, ... of the kv_mul * hs accumulators
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int n_out = kv_mul * hs;
     for (int t0 = t_begin; t0 < t_end; t0 += ATT_SUB) {
         const int T = min(ATT_SUB, t_end - t0);
-        __syncthreads();
-        const int hs4 = hs / 4;
-        for (int i = tid; i < T * hs4; i += nt) {
-            const int t = i / hs4, c = i - t * hs4;
-            const size_t g = (size_t)(t0 + t) * a.kv_dim + (size_t)kvh * hs + 4 * c;
-            ((float4 *)sk)[i] = *(const float4 *)(a.kc + g);
-            ((float4 *)sv)[i] = *(const float4 *)(a.vc + g);
+#pragma unroll
+        for (int k = 0; k < ATT_VEC; k++) {
+            int t, c;
+            kv_index(t0, k, &t, &c);
+            *(f32x4 *)(sk + t * ks + 4 * c) = rk[k];
+            *(f32x4 *)(sv + t * hs + 4 * c) = rv[k];
         }
         __syncthreads();
+        KERNEL_MARK(1);
+        if (t0 + ATT_SUB < t_end) load_kv(t0 + ATT_SUB);
         for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), i in order
             const int j = i / T, t = i - j * T;
-            const float *qq = sq + j * hs, *kk = sk + t * hs;
+            const float *qq = sq + j * hs, *kk = sk + t * ks;
             float d = 0.0f;
             for (int e = 0; e < hs; e++) d += qq[e] * kk[e];
             sc[j * ATT_SUB + t] = d / rs;
@@ -463,11 +614,11 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
         __syncthreads();
         for (int j = wave; j < kv_mul; j += nw) { // online softmax statistics, one wave per head
             float v = lane < T ? sc[j * ATT_SUB + lane] : -INFINITY;
-            float mx = group_max(v, WAVE);
+            float mx = wave_max(v);
             const float m_old = sm_[j], m_new = fmaxf(m_old, mx);
             const float e = lane < T ? expf(v - m_new) : 0.0f;
             if (lane < T) sc[j * ATT_SUB + lane] = e;
-            const float sum = wave_sum_from(e, 1);
+            const float sum = wave_sum(e);
             if (lane == 0) {
                 const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
                 sf[j] = f;
@@ -476,6 +627,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             }
         }
         __syncthreads();
+        KERNEL_MARK(2);
         for (int k = 0; k < 4; k++) {
             const int o = tid + k * nt;
             if (o < n_out) {
@@ -485,6 +637,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
                 acc[k] = v;
             }
         }
+        __syncthreads(); // the next sub-chunk's stores overwrite sk, sv and sc
     }
     for (int k = 0; k < 4; k++) {
         const int o = tid + k * nt;
@@ -498,12 +651,16 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
         ml[0] = sm_[tid];
         ml[1] = sl[tid];
     }
+    KERNEL_MARK(3);
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv, threads = 256;
-    if (kv_mul * a.hs > 4 * threads || a.hs % 4) return hipErrorInvalidValue;
-    const size_t lds = ((size_t)kv_mul * a.hs + 2 * (size_t)ATT_SUB * a.hs + (size_t)kv_mul * ATT_SUB + 3 * kv_mul) * 4;
+    if (kv_mul * a.hs > 4 * threads || a.hs % 4 || a.hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) ||
+        ((uintptr_t)a.vc & 15) || (a.kv_dim % 4))
+        return hipErrorInvalidValue;
+    const size_t lds =
+        ((size_t)kv_mul * a.hs + (size_t)ATT_SUB * (2 * a.hs + 4) + (size_t)kv_mul * ATT_SUB + 3 * kv_mul) * 4;
     hipLaunchKernelGGL(k_attention, dim3(a.n_kv * a.splits), dim3(threads), lds, st, a);
     return hipGetLastError();
 }

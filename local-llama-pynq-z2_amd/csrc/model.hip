@@ -36,7 +36,7 @@ struct Layer {
 };
 
 enum { K_EMBED, K_QKV, K_ATTN, K_O, K_GU, K_DOWN, K_HEAD, K_ARGMAX, K_COUNT };
-const char *k_names[K_COUNT] = {"embed", "qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv",
+const char *k_names[K_COUNT] = {"step_start", "qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv",
                                 "head_gemv", "argmax"};
 
 struct Prof { // events around every launch of a step

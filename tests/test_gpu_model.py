@@ -130,7 +130,7 @@ def test_decode_replay_and_profile_run():
     assert ms > 0
     st = m.profile(4)
     names = {s["name"] for s in st}
-    assert {"qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv"} <= names
+    assert {"step_start", "qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv"} <= names
     m.close()
 
 

@@ -82,7 +82,7 @@ def run_matvec4(drv, w, s, xq, xs, n, d, bits):
 
 QUICK = [(96, 5, 4), (96, 5, 8), (896, 128, 4), (896, 64, 8), (4864, 32, 4), (8192, 4, 4)]
 ALL = [(896, 896, 4), (896, 128, 4), (896, 4864, 4), (4864, 896, 4), (896, 49152, 8), (18944, 512, 4),
-       (3584, 1024, 8)]
+       (3584, 1024, 8), (32768, 24, 4), (32768, 24, 8)]
 
 
 @pytest.mark.parametrize("n,d,bits", QUICK + ALL)
@@ -129,7 +129,9 @@ def test_matvec4_golden(drv, k):
 
 
 MATVEC_TB = [(288, 288, 32), (288, 768, 32), (768, 288, 32), (768, 768, 64), (768, 2048, 64), (2048, 768, 64),
-             (768, 32000, 64), (96, 7, 32), (768, 32000, 32)]
+             (768, 32000, 64), (96, 7, 32), (768, 32000, 32),
+             # the largest n (MATVEC_HIP_MAX_N): activations take more than one prologue pass per thread
+             (32768, 40, 64), (32768, 9, 32)]
 
 
 @pytest.mark.parametrize("n,d,gs", MATVEC_TB)
@@ -150,6 +152,27 @@ def test_matvec_runq_bit_exact(drv, n, d, gs):
     ref = np.empty(d, np.float32)
     oracle().or_matvec_runq(ptr(ref), ptr(wq), ptr(ws), ptr(xq), ptr(xs), n, d, gs)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("offset", [4, 8, 12])
+def test_matvec_runq_unaligned_activations(drv, offset):
+    """xq at a device address that is only 4-byte aligned (the reference checks no alignment, matvec_fpga.cpp:178-182)"""
+    n, d, gs = 768, 96, 32
+    rng = np.random.default_rng(99 + offset)
+    wq = rng.integers(-128, 128, size=d * n, dtype=np.int8)
+    xq = rng.integers(-128, 128, size=n, dtype=np.int8)
+    ws = rng.uniform(1e-4, 2e-2, size=d * n // gs).astype(np.float32)
+    xs = rng.uniform(1e-3, 1e-1, size=n // gs).astype(np.float32)
+    _, pw = drv.put(wq)
+    _, ps = drv.put(ws)
+    xbuf, px = drv.alloc(n + 64)
+    xbuf[offset:offset + n] = xq.view(np.uint8)
+    _, pxs = drv.put(xs)
+    out, po = drv.alloc(d * 4)
+    assert drv.matvec(pw, ps, px + offset, pxs, po, n, d, gs) == 0
+    ref = np.empty(d, np.float32)
+    oracle().or_matvec_runq(ptr(ref), ptr(wq), ptr(ws), ptr(xq), ptr(xs), n, d, gs)
+    assert np.array_equal(out.view(np.float32)[:d].view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("k", range(3))
