@@ -75,9 +75,9 @@ typedef struct {
 } llm_kernel_stat;
 int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int max_stats);
 
-/* Batched prompt processing (prefill): positions 0..n-1 in one pass, int8 MFMA GEMMs for the layer
- * matrices and causal attention; fills the KV cache like n forward() calls would and leaves the logits of
- * the last position in `logits` (n_logits floats, may be NULL).  .qwb models only.  Returns 0 or -1. */
+/* Prompt processing (prefill): positions 0..n-1 in one call; fills the KV cache like n forward() calls
+ * would and leaves the logits of the last position in `logits` (n_logits floats, may be NULL).  Runs one
+ * decode step per position.  Returns 0 or -1. */
 int llm_prefill(llm_model *m, const int *ids, int n, float *logits);
 
 void llm_close(llm_model *m);
