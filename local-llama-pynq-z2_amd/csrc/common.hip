@@ -3,31 +3,52 @@
 
 #include "host_common.h"
 
-// Shapes follow from the tiled matrix: a row-block has `nchunks` chunk records of 1 KiB+ each.  The chunks of
-// a row-block are split over kw waves so that each wave holds at most a few batches, and one block takes
-// one iteration (row-blocks of one block: nb), so that the whole grid's loads are in flight at once and a
-// block's latency chain is one load round trip plus its prologue.  Epilogues that need whole groups of rows
-// fix nb: SwiGLU quantizes gs hidden values per group, each row-block yields rb/2 of them.
-GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered) {
-    (void)pro;
-    GemvShape s;
-    const int C = T.nchunks;
-    if (ordered) {
-        s.kw = 1;
-        s.nb = 4;
-    } else {
-        s.kw = (C + 3) / 4;
-        if (s.kw > 16) s.kw = 16;
-        if (s.kw < 1) s.kw = 1;
-        s.nb = 4 / s.kw > 1 ? 4 / s.kw : 1;
-    }
+// Shapes follow from the tiled matrix: a row-block has `nchunks` chunk records of 1 KiB+ each; its chunks are
+// split over kw waves, and an iteration is nb row-blocks.  Epilogues that need whole groups of rows fix nb:
+// SwiGLU quantizes gs hidden values per group, each row-block yields rb/2 of them.
+//   Latency shape (when every iteration's block fits on the chip at once, 16 waves per CU): about 4 chunks
+//   per wave and one iteration per block, so all loads are in flight together and a block's latency chain
+//   is one round trip plus its prologue.
+//   Streaming shape (larger matrices): about 16 chunks per wave, blocks of at least 4 waves, and a
+//   persistent grid of as many blocks as fit at once; each block pays its prologue once and streams its
+//   iterations back to back.
+static void gemv_split(GemvShape &s, int C, int per_wave, const TiledMat &T, int epi) {
+    s.kw = (C + per_wave - 1) / per_wave;
+    if (s.kw > 16) s.kw = 16;
+    if (s.kw < 1) s.kw = 1;
+    s.nb = 4 / s.kw > 1 ? 4 / s.kw : 1;
     if (epi == EPI_SWIGLU) {
         s.nb = T.gs / (T.rb / 2);
         if (s.nb * s.kw > 16) s.kw = 16 / s.nb;
         if (s.kw < 1) s.kw = 1;
     }
-    const int iters = (T.nblocks + s.nb - 1) / s.nb;
-    s.grid = iters < 65535 ? iters : 65535;
+}
+
+GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus) {
+    (void)pro;
+    GemvShape s;
+    const int C = T.nchunks;
+    if (cus < 1) cus = 1;
+    if (ordered) {
+        s.kw = 1;
+        s.nb = 4;
+    } else {
+        gemv_split(s, C, 4, T, epi);
+    }
+    int iters = (T.nblocks + s.nb - 1) / s.nb;
+    int waves = s.kw * s.nb;
+    int resident = cus * (waves < 16 ? 16 / waves : 1);
+    if (iters > resident) {
+        if (!ordered) {
+            gemv_split(s, C, 16, T, epi);
+            iters = (T.nblocks + s.nb - 1) / s.nb;
+            waves = s.kw * s.nb;
+            resident = cus * (waves < 16 ? 16 / waves : 1);
+        }
+        s.grid = iters > resident ? resident : iters;
+    } else {
+        s.grid = iters;
+    }
     if (s.grid < 1) s.grid = 1;
     return s;
 }

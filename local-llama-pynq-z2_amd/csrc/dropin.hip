@@ -106,7 +106,7 @@ const Weight *weight(const char *who, uint64_t w, uint64_t ws, int n, int d, int
         hipFree(x.tiled);
         return nullptr;
     }
-    x.shape = gemv_pick_shape(x.T, PRO_XQ, EPI_STORE, ordered);
+    x.shape = gemv_pick_shape(x.T, PRO_XQ, EPI_STORE, ordered, hip_cu_count(S.device));
     S.weights.push_back(x);
     return &S.weights.back();
 }

@@ -31,11 +31,22 @@ static inline int hip_device_from_env(const char *who) {
 }
 
 // GEMV launch shape for a tiled matrix: waves per row-block (K split inside the block), row-blocks per
-// block iteration, and the grid.  `ordered` keeps each row's groups in one lane, summed in order.
+// block iteration, and the grid.  `ordered` keeps each row's groups in one lane, summed in order.  `cus` is
+// the device's compute-unit count (hip_cu_count).
 struct GemvShape {
     int kw, nb, grid;
 };
-GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered);
+GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus);
+
+// Compute units of device `dev` (0 with a message on failure).
+static inline int hip_cu_count(int dev) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        fprintf(stderr, "hip: cannot read the compute-unit count of device %d\n", dev);
+        return 0;
+    }
+    return n;
+}
 // Row-block size for a plain matrix of d rows x n inputs (fused QKV and gate/up keep 16 for their pairing).
 int gemv_row_block(int d, int n);
 

@@ -220,14 +220,33 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
 
     asm volatile("" ::: "memory"); // keep the issue order: prologue operands, then weights
 
-    // (2) weights of this block's first iteration
+    // (2) the wave's first two weight batches.  The batches of all the block's iterations (it0, it0 + grid,
+    // ...) form one stream per wave: bpi batches per iteration, two buffers, and the next iteration's first
+    // batch is in flight while the current one is reduced and finished.
+    const int cnt_w = (W.nchunks - my_kw + a.kw - 1) / a.kw;     // chunks of a row-block for this wave (>= 1)
+    const int bpi = (cnt_w + F::UNROLL - 1) / F::UNROLL;         // batches per iteration
+    const int n_my = it0 < n_it ? (n_it - 1 - it0) / (int)gridDim.x + 1 : 0;
+    const int total = n_my * bpi;
+    float pre_x = 0.0f, pre_x_next = 0.0f; // EPI_RESID: out[R] of this / the next iteration's row
+    int iss_it = it0, iss_bi = 0;          // the next batch to issue
+    auto issue = [&](uint4 (&w)[F::UNROLL][F::PIECES], uint32_t (&sr)[F::UNROLL]) {
+        const int b = min(iss_it * a.nb + my_nb, W.nblocks - 1);
+        load_batch<WB, GSZ, SF32>(W.data + (size_t)b * W.nchunks * W.rec, W.rec, W.nchunks,
+                                  my_kw + iss_bi * F::UNROLL * a.kw, a.kw, lane, w, sr);
+        if constexpr (EPI == EPI_RESID)
+            if (iss_bi == 0 && iss_it != it0) pre_x_next = a.out[min(iss_it * rows_it + tid, W.rows - 1)];
+        if (++iss_bi == bpi) {
+            iss_bi = 0;
+            iss_it += gridDim.x;
+        }
+    };
     uint4 wa[F::UNROLL][F::PIECES], wb[F::UNROLL][F::PIECES];
     uint32_t sa[F::UNROLL], sb[F::UNROLL];
-    load_batch<WB, GSZ, SF32>(W.data + (size_t)min(it0 * a.nb + my_nb, W.nblocks - 1) * W.nchunks * W.rec, W.rec,
-                              W.nchunks, my_kw, a.kw, lane, wa, sa);
+    if (total > 0) issue(wa, sa);
+    if (total > 1) issue(wb, sb);
 
     // (3) the epilogue operands of this thread's first row (clamped row index, used only for valid rows)
-    float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f, pre_x = 0.0f;
+    float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f;
     {
         const int R = min(it0 * rows_it + tid, W.rows - 1);
         if constexpr (EPI == EPI_RESID) pre_x = a.out[R];
@@ -249,6 +268,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
         }
     }
 
+    KERNEL_MARK(1);
     // (4) prologue: int8 activations and their scales into LDS
     if constexpr (PRO == PRO_XQ) {
         const int nq = n / 16;
@@ -286,6 +306,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
                 part += v.z * v.z;
                 part += v.w * v.w;
             }
+            KERNEL_MARK(2);
             float ss = block_sum(part, sred);
             ss /= (float)n;
             ss += a.eps;
@@ -312,6 +333,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
                               nh, wgt);
             }
             __syncthreads();
+            KERNEL_MARK(2);
             // value slots of 4 elements: sum over slices in slice order
             const int nv = n / 4;
             for (int v0 = 0; v0 < nv; v0 += nt) {
@@ -337,6 +359,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             }
         }
         __syncthreads();
+        KERNEL_MARK(3);
         block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
         for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
     }
@@ -344,29 +367,13 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     if constexpr (PRO == PRO_XQ)
         for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
     __syncthreads();
-    KERNEL_MARK(1);
+    KERNEL_MARK(4);
 
-    // (4) main loop over iterations (usually one per block), batches double-buffered
+    // (5) reduction and epilogue of iteration `it` (every wave calls it once per iteration: barriers inside)
     float best_v = -INFINITY;
     int best_i = 0x7fffffff;
-    for (int it = it0; it < n_it; it += gridDim.x) {
-        const int b = it * a.nb + my_nb;
-        float acc = 0.0f;
-        if (b < W.nblocks) {
-            const uint8_t *base = W.data + (size_t)b * W.nchunks * W.rec;
-            const int step = a.kw * F::UNROLL;
-            if (it != it0) load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, my_kw, a.kw, lane, wa, sa);
-            for (int c0 = my_kw;; c0 += 2 * step) {
-                if (c0 + step < W.nchunks) load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, c0 + step, a.kw, lane, wb, sb);
-                acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, c0, a.kw, gpc, g_lane, sxq, sxs, wa, sa);
-                if (c0 + step >= W.nchunks) break;
-                if (c0 + 2 * step < W.nchunks)
-                    load_batch<WB, GSZ, SF32>(base, W.rec, W.nchunks, c0 + 2 * step, a.kw, lane, wa, sa);
-                acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, c0 + step, a.kw, gpc, g_lane, sxq, sxs, wb, sb);
-                if (c0 + 2 * step >= W.nchunks) break;
-            }
-        }
-        KERNEL_MARK(2);
+    auto finish = [&](int it, float acc) {
+        KERNEL_MARK(5);
         acc = wave_sum_from(acc, rb); // lanes holding the same row
         if (lane < rb) sred[wave * rb + lane] = acc;
         __syncthreads();
@@ -377,14 +384,15 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             srow[tid] = v;
         }
         __syncthreads();
+        KERNEL_MARK(6);
 
-        // ---- epilogue
         const int R = it * rows_it + tid; // logical row of this thread
         const bool first_it = it == it0;
         if constexpr (EPI == EPI_STORE) {
             if (tid < rows_it && R < W.rows) a.out[R] = srow[tid];
         } else if constexpr (EPI == EPI_RESID) {
-            if (tid < rows_it && R < W.rows) a.out[R] = (first_it ? pre_x : a.out[R]) + srow[tid]; // qwen.c:551, 565
+            if (tid < rows_it && R < W.rows) a.out[R] = pre_x + srow[tid]; // qwen.c:551, 565
+            pre_x = pre_x_next;
         } else if constexpr (EPI == EPI_ARGMAX) {
             if (tid < rows_it && R < W.rows) {
                 const float v = srow[tid];
@@ -460,6 +468,28 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             }
         }
         __syncthreads();
+    };
+
+    // (6) the stream: consume a batch, refill its buffer with the batch two ahead
+    int use_it = it0, use_bi = 0;
+    float acc = 0.0f;
+    auto consume = [&](const uint4 (&w)[F::UNROLL][F::PIECES], const uint32_t (&sr)[F::UNROLL]) {
+        if (use_it * a.nb + my_nb < W.nblocks)
+            acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, my_kw + use_bi * F::UNROLL * a.kw, a.kw, gpc, g_lane, sxq,
+                                          sxs, w, sr);
+        if (++use_bi == bpi) {
+            finish(use_it, acc);
+            acc = 0.0f;
+            use_bi = 0;
+            use_it += gridDim.x;
+        }
+    };
+    for (int q = 0; q < total; q += 2) {
+        consume(wa, sa);
+        if (q + 2 < total) issue(wa, sa);
+        if (q + 1 >= total) break;
+        consume(wb, sb);
+        if (q + 3 < total) issue(wb, sb);
     }
     if constexpr (EPI == EPI_ARGMAX) {
         // block argmax: larger value wins, equal values keep the lower row (first strict maximum)
@@ -480,7 +510,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             a.part_idx[blockIdx.x] = i;
         }
     }
-    KERNEL_MARK(3);
+    KERNEL_MARK(7);
 }
 
 size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
@@ -589,6 +619,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
     asm volatile("" ::: "memory"); // every load above is issued before the first store waits for one
     ((f32x4 *)sq)[min(tid, nq4 - 1)] = rq;
     if (tid < kv_mul) { sm_[tid] = -INFINITY; sl[tid] = 0.0f; }
+    KERNEL_MARK(1);
     // each thread owns outputs (j, e) = o, o + nt, ... of the kv_mul * hs accumulators
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int n_out = kv_mul * hs;
@@ -602,7 +633,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             *(f32x4 *)(sv + t * hs + 4 * c) = rv[k];
         }
         __syncthreads();
-        KERNEL_MARK(1);
+        KERNEL_MARK(2);
         if (t0 + ATT_SUB < t_end) load_kv(t0 + ATT_SUB);
         for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), i in order
             const int j = i / T, t = i - j * T;
@@ -612,6 +643,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             sc[j * ATT_SUB + t] = d / rs;
         }
         __syncthreads();
+        KERNEL_MARK(3);
         for (int j = wave; j < kv_mul; j += nw) { // online softmax statistics, one wave per head
             float v = lane < T ? sc[j * ATT_SUB + lane] : -INFINITY;
             float mx = wave_max(v);
@@ -627,7 +659,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             }
         }
         __syncthreads();
-        KERNEL_MARK(2);
+        KERNEL_MARK(4);
         for (int k = 0; k < 4; k++) {
             const int o = tid + k * nt;
             if (o < n_out) {
@@ -638,6 +670,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
             }
         }
         __syncthreads(); // the next sub-chunk's stores overwrite sk, sv and sc
+        KERNEL_MARK(5);
     }
     for (int k = 0; k < 4; k++) {
         const int o = tid + k * nt;
@@ -651,7 +684,7 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
         ml[0] = sm_[tid];
         ml[1] = sl[tid];
     }
-    KERNEL_MARK(3);
+    KERNEL_MARK(7);
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {

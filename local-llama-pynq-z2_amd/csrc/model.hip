@@ -351,15 +351,17 @@ struct Src { const uint8_t *w, *s; };
 
 int finish_setup(llm_model *m) {
     const llm_info &I = m->info;
+    const int cus = hip_cu_count(m->device);
+    if (!cus) return -1;
     // per-layer shapes
     for (Layer &ly : m->L) {
         const int ord = m->kind == 1;
-        ly.s_qkv = gemv_pick_shape(ly.qkv, PRO_NORM, EPI_QKV, ord);
-        ly.s_o = gemv_pick_shape(ly.o, PRO_ATTN, EPI_RESID, ord);
-        ly.s_gu = gemv_pick_shape(ly.gu, PRO_NORM, EPI_SWIGLU, ord);
-        ly.s_down = gemv_pick_shape(ly.down, PRO_XQ, EPI_RESID, ord);
+        ly.s_qkv = gemv_pick_shape(ly.qkv, PRO_NORM, EPI_QKV, ord, cus);
+        ly.s_o = gemv_pick_shape(ly.o, PRO_ATTN, EPI_RESID, ord, cus);
+        ly.s_gu = gemv_pick_shape(ly.gu, PRO_NORM, EPI_SWIGLU, ord, cus);
+        ly.s_down = gemv_pick_shape(ly.down, PRO_XQ, EPI_RESID, ord, cus);
     }
-    m->s_head = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, m->kind == 1);
+    m->s_head = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, m->kind == 1, cus);
     // attention slices: up to 64 per kv head, each at least ATT_SUB positions
     m->att_splits = (m->ctx + ATT_SUB - 1) / ATT_SUB;
     if (m->att_splits > 64) m->att_splits = 64;
