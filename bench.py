@@ -6,7 +6,8 @@ with seeded head_ids; seeded N(0, 0.02) random-init weights written by host/synt
 greedy, batch 1.  A step is one decode position: the whole forward() plus the argmax on the device, one
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
-  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c3|c5] [--no-cpu]
+  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c3|c4|c5] [--no-cpu]
+  (c4: the 512-token prompt as one batched int8-MFMA prefill, timed over --steps repetitions)
 
 Also reported: per-kernel roofline (HIP events around every launch on the library's stream, algorithmic
 bytes per launch), the greedy ids against the reference's own qwen.c, and that qwen.c (built with OpenMP,
@@ -29,6 +30,9 @@ CONFIGS = {
     "c3": dict(preset="c3", seed=3, prompt=24, new=128, ctx=1024,
                workload="Qwen2-0.5B shape .qwb decode (dim 896, 24 layers, 14/2 heads, FFN 4864, Q4_0 layers, "
                         "Q8_0 65536-row head): 24-token prompt, 128 greedy tokens, batch 1"),
+    "c4": dict(preset="c3", seed=3, prompt=512, new=64, ctx=1024,
+               workload="Qwen2-0.5B shape .qwb prefill (dim 896, 24 layers, 14/2 heads, FFN 4864, Q4_0 layers): "
+                        "512-token prompt as int8 MFMA GEMMs + causal attention, then 64 greedy tokens, batch 1"),
     "c5": dict(preset="c5", seed=5, prompt=32, new=256, ctx=4096,
                workload="Qwen2-7B shape .qwb decode (dim 3584, 28 layers, 28/4 heads of 128, FFN 18944, Q4_0 "
                         "layers, Q8_0 152064-row head): 32-token prompt, 256 greedy tokens, KV cache 4096, batch 1"),
@@ -119,6 +123,46 @@ def greedy_parity(path, prompt, n_new, ctx, ids_gpu, logits_gpu):
     return out
 
 
+def layer_macs(info):
+    """multiply-accumulates of the layer matrices for one token (qkv, o, gate/up, down)"""
+    kv = info.dim // info.n_heads * info.n_kv_heads
+    return info.n_layers * info.dim * (info.dim + 2 * kv + info.dim + 3 * info.hidden_dim)
+
+
+def prefill_bench(a, cfg, path, prompt):
+    """C4: the prompt as one batched prefill, timed over `steps` repetitions; int8 ops counted on the layer GEMMs"""
+    import torch
+    P = load_pkg()
+    m = P.Model(path, cfg["ctx"])
+    reps = a.steps or 5
+    m.prefill(prompt)  # warmup (and the activation buffers)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        m.prefill(prompt)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps
+    tok_s = len(prompt) / wall
+    ops = 2.0 * layer_macs(m.info) * len(prompt)
+    log(f"prefill of {len(prompt)} tokens: {wall * 1e3:.2f} ms -> {tok_s:.0f} tok/s, layer GEMMs {ops / 1e9:.1f} G int8 "
+        f"ops = {ops / wall / 1e12:.1f} TOP/s over the whole prefill")
+    gen = m.generate(prompt, cfg["new"])
+    log(f"then {len(gen['ids'])} greedy tokens, decode {gen['timing'].decode_ms:.1f} ms")
+    m.close()
+    PEAK_I8 = 5000.0  # TOP/s, dense int8 MFMA
+    out = {
+        "metric": "prefill tok/s (int8 MFMA), Q4_0 Qwen2-0.5B shape, 512-token prompt",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic: seeded N(0,0.02) random-init weights, seeded prompt ids",
+        "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "ctx": cfg["ctx"], "batch": 1},
+        "roofline": {"bound": "mfma", "achieved": round(ops / wall / 1e12, 2), "peak": PEAK_I8, "unit": "TFLOP/s",
+                     "frac": round(ops / wall / 1e12 / PEAK_I8, 5), "traffic": None,
+                     "note": "int8 ops of the layer GEMMs over the whole prefill time (every kernel included)"},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +186,8 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.init()
+    if a.config == "c4":
+        return prefill_bench(a, cfg, path, prompt)
     P = load_pkg()
     t = time.time()
     m = P.Model(path, cfg["ctx"])

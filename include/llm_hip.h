@@ -75,10 +75,16 @@ typedef struct {
 } llm_kernel_stat;
 int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int max_stats);
 
-/* Prompt processing (prefill): positions 0..n-1 in one call; fills the KV cache like n forward() calls
- * would and leaves the logits of the last position in `logits` (n_logits floats, may be NULL).  Runs one
- * decode step per position.  Returns 0 or -1. */
+/* Batched prompt processing (prefill; the reference runs the prompt one forward() per position,
+ * qwen.c:674-681): positions 0..n-1 pass through each layer together, in chunks of up to 512 tokens.  The
+ * layer matrices become int8 MFMA GEMMs with exact int32 group sums and the reference's per-group product
+ * and group order; attention is causal over the KV cache.  Fills the KV cache like n forward() calls and
+ * leaves the logits of position n-1 in `logits` (n_logits floats, may be NULL); the step state is then
+ * position n-1.  Returns 0 or -1. */
 int llm_prefill(llm_model *m, const int *ids, int n, float *logits);
+/* Whether llm_generate runs the prompt through llm_prefill (on by default) or one decode step per prompt
+ * position.  The --logits history (llm_generate with `logits`) always uses the per-position steps. */
+int llm_set_prefill(llm_model *m, int on);
 
 void llm_close(llm_model *m);
 
@@ -90,6 +96,11 @@ int mvh_quantize(const float *x, int n, int flavor, int gs, int8_t *q, float *s)
 /* exact int32 group sums of a matrix in the reference layout (qwen planes: bits 4 or 8, group 32; or runq
  * int8 with group gs when bits == 0), computed by the GEMV kernels' own dot-product code: ival[d][n/gs] */
 int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, int bits, int gs, int32_t *ival);
+/* the prefill GEMM on caller data: y[m][r] for M tokens, weights in the reference layout (qwen planes: bits 4
+ * or 8 with fp16 scales, group 32; runq: bits 0 = int8 with fp32 scales, group gs), tiled with row-blocks of
+ * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d] */
+int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
+                     int bits, int gs, int rb, float *y);
 /* device state after the last llm_forward/llm_generate step: 0 = residual stream x (dim floats, after the
  * final rmsnorm like qwen.c:569), 1 = key cache of layer `layer` (ctx * kv_dim), 2 = value cache */
 int llm_read_state(llm_model *m, int which, int layer, float *dst, size_t count);

@@ -77,6 +77,8 @@ def lib():
     L.llm_read_state.argtypes = [vp, i32, i32, vp, sz]
     L.mvh_quantize.argtypes = [vp, i32, i32, i32, vp, vp]
     L.mvh_group_dots.argtypes = [vp, vp, i32, i32, i32, i32, vp]
+    L.mvh_prefill_gemm.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
+    L.llm_set_prefill.argtypes = [vp, i32]
     _lib = L
     return L
 
@@ -105,6 +107,19 @@ def group_dots(w, xq, n, d, bits, gs=32):
     if lib().mvh_group_dots(_ptr(w), _ptr(xq), n, d, bits, gs, _ptr(out)) != 0:
         raise RuntimeError("mvh_group_dots failed")
     return out
+
+
+def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16):
+    """The prefill GEMM (int8 MFMA) on caller data: [M, d] float32.  bits 4/8: qwen planes with fp16 scales;
+    bits 0: runq int8 with fp32 scales, group gs."""
+    w = np.ascontiguousarray(w).view(np.uint8)
+    ws = np.ascontiguousarray(ws)
+    xq = np.ascontiguousarray(xq, dtype=np.int8)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    y = np.empty((M, d), np.float32)
+    if lib().mvh_prefill_gemm(_ptr(w), _ptr(ws), _ptr(xq), _ptr(xs), M, n, d, bits, gs, rb, _ptr(y)) != 0:
+        raise RuntimeError("mvh_prefill_gemm failed")
+    return y
 
 
 # ---- drop-in driver API -----------------------------------------------------------------------------------
@@ -206,7 +221,12 @@ class Model:
             raise RuntimeError("llm_read_state failed")
         return out
 
+    def set_prefill(self, on):
+        """whether generate() runs the prompt as one batched prefill (default) or one step per position"""
+        self.L.llm_set_prefill(self.h, 1 if on else 0)
+
     def prefill(self, ids):
+        """batched prefill of positions 0..len(ids)-1; the logits of the last position"""
         p = np.ascontiguousarray(ids, dtype=np.int32)
         lg = np.empty(self.info.n_logits, np.float32)
         if self.L.llm_prefill(self.h, _ptr(p), len(p), _ptr(lg)) != 0:

@@ -1,0 +1,125 @@
+// Attention of one kv head's query heads over a range of positions (device code shared by the decode and
+// prefill kernels of libmatvec_hip.so; internal header).
+//
+// qwen.c:526-546 / runq.c:530-568: score_t = (q . k_t) / sqrtf(hs) as a sequential dot in the reference's
+// order, softmax, weighted sum of V.  Here the softmax is online over sub-chunks of ATT_SUB positions (running
+// max and sum, rescaled partial sums), K and V staged in LDS.
+#pragma once
+#include "device.h"
+#include "kernels.h"
+
+#ifndef KERNEL_MARK
+#define KERNEL_MARK(k)
+#endif
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vectors per thread for one sub-chunk of K (and as many of V): ATT_SUB * hs / 4 <= ATT_VEC * 256
+#define ATT_VEC 4
+
+// LDS floats of attn_range for kv_mul query heads of size hs.  K rows are padded to hs + 4 floats: the score
+// loop's lanes read different rows at the same column, which a power-of-two stride would put in one bank.
+__host__ __device__ inline size_t attn_lds_floats(int kv_mul, int hs) {
+    return (size_t)kv_mul * hs + (size_t)ATT_SUB * (2 * hs + 4) + (size_t)kv_mul * ATT_SUB + 3 * (size_t)kv_mul;
+}
+
+// Block of 256 threads.  q: the kv_mul * hs query values of kv head kvh (16-byte aligned); kc, vc: the layer's
+// caches [ctx][kv_dim].  On return acc[k] holds the exp-weighted value sum of output (j, e) = tid + 256 k
+// (head j of the group, element e) and ml_max / ml_sum point at the kv_mul running maxima / sums in LDS.
+// Every thread of the block must call it (barriers inside); t_begin < t_end.
+__device__ __forceinline__ void attn_range(const float *q, const float *kc, const float *vc, int kv_dim, int kvh,
+                                           int hs, int kv_mul, int t_begin, int t_end, float *sm, float (&acc)[4],
+                                           const float **ml_max, const float **ml_sum) {
+    const int hs4 = hs / 4, tid = threadIdx.x, nt = blockDim.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid & (WAVE - 1), nw = nt / WAVE;
+    const int ks = hs + 4;
+    float *sq = sm;                          // kv_mul * hs
+    float *sk = sq + kv_mul * hs;            // ATT_SUB * ks
+    float *sv = sk + ATT_SUB * ks;           // ATT_SUB * hs
+    float *sc = sv + ATT_SUB * hs;           // kv_mul * ATT_SUB scores, then exponentials
+    float *sm_ = sc + kv_mul * ATT_SUB;      // kv_mul running max
+    float *sl = sm_ + kv_mul;                // kv_mul running sum
+    float *sf = sl + kv_mul;                 // kv_mul rescale factor of this step
+    const float rs = sqrtf((float)hs);
+
+    // Every global load of a sub-chunk is issued before the first is waited for: q of the kv_mul heads with
+    // the first sub-chunk, each later sub-chunk while the previous one is computed.  Vector indices past
+    // the end are clamped; their stores write the last vector's own value again.
+    const int nq4 = kv_mul * hs4; // <= nt
+    const f32x4 rq = ((const f32x4 *)q)[min(tid, nq4 - 1)];
+    f32x4 rk[ATT_VEC], rv[ATT_VEC];
+    // vector k of this thread in a sub-chunk: row t, column vector c (clamped to the sub-chunk's last)
+    auto kv_index = [&](int t0, int k, int *t, int *c) {
+        const int cnt = min(ATT_SUB, t_end - t0) * hs4, i = min(tid + k * nt, cnt - 1);
+        *t = i / hs4;
+        *c = i - *t * hs4;
+    };
+    auto load_kv = [&](int t0) {
+#pragma unroll
+        for (int k = 0; k < ATT_VEC; k++) {
+            int t, c;
+            kv_index(t0, k, &t, &c);
+            const size_t gi = (size_t)(t0 + t) * kv_dim + (size_t)kvh * hs + 4 * c;
+            rk[k] = *(const f32x4 *)(kc + gi);
+            rv[k] = *(const f32x4 *)(vc + gi);
+        }
+    };
+    load_kv(t_begin);
+    asm volatile("" ::: "memory"); // every load above is issued before the first store waits for one
+    ((f32x4 *)sq)[min(tid, nq4 - 1)] = rq;
+    if (tid < kv_mul) { sm_[tid] = -INFINITY; sl[tid] = 0.0f; }
+    KERNEL_MARK(1);
+    // each thread owns outputs (j, e) = o, o + nt, ... of the kv_mul * hs accumulators
+    for (int k = 0; k < 4; k++) acc[k] = 0.0f;
+    const int n_out = kv_mul * hs;
+    for (int t0 = t_begin; t0 < t_end; t0 += ATT_SUB) {
+        const int T = min(ATT_SUB, t_end - t0);
+#pragma unroll
+        for (int k = 0; k < ATT_VEC; k++) {
+            int t, c;
+            kv_index(t0, k, &t, &c);
+            *(f32x4 *)(sk + t * ks + 4 * c) = rk[k];
+            *(f32x4 *)(sv + t * hs + 4 * c) = rv[k];
+        }
+        __syncthreads();
+        KERNEL_MARK(2);
+        if (t0 + ATT_SUB < t_end) load_kv(t0 + ATT_SUB);
+        for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), i in order
+            const int j = i / T, t = i - j * T;
+            const float *qq = sq + j * hs, *kk = sk + t * ks;
+            float d = 0.0f;
+            for (int e = 0; e < hs; e++) d += qq[e] * kk[e];
+            sc[j * ATT_SUB + t] = d / rs;
+        }
+        __syncthreads();
+        KERNEL_MARK(3);
+        for (int j = wave; j < kv_mul; j += nw) { // online softmax statistics, one wave per head
+            float v = lane < T ? sc[j * ATT_SUB + lane] : -INFINITY;
+            float mx = wave_max(v);
+            const float m_old = sm_[j], m_new = fmaxf(m_old, mx);
+            const float e = lane < T ? expf(v - m_new) : 0.0f;
+            if (lane < T) sc[j * ATT_SUB + lane] = e;
+            const float sum = wave_sum(e);
+            if (lane == 0) {
+                const float f = m_old == -INFINITY ? 0.0f : expf(m_old - m_new);
+                sf[j] = f;
+                sl[j] = sl[j] * f + sum;
+                sm_[j] = m_new;
+            }
+        }
+        __syncthreads();
+        KERNEL_MARK(4);
+        for (int k = 0; k < 4; k++) {
+            const int o = tid + k * nt;
+            if (o < n_out) {
+                const int j = o / hs, e = o - j * hs;
+                float v = acc[k] * sf[j];
+                for (int t = 0; t < T; t++) v += sc[j * ATT_SUB + t] * sv[t * hs + e];
+                acc[k] = v;
+            }
+        }
+        __syncthreads(); // the next sub-chunk's stores overwrite sk, sv and sc
+        KERNEL_MARK(5);
+    }
+    *ml_max = sm_;
+    *ml_sum = sl;
+}

@@ -5,6 +5,7 @@
 
 #include "../../include/llm_hip.h"
 #include "host_common.h"
+#include "prefill.h"
 
 namespace {
 int hook_device(const char *who) {
@@ -82,6 +83,65 @@ extern "C" int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, 
     hipFree(dt);
     hipFree(dx);
     hipFree(di);
+    hipFree(dmap);
+    return rc;
+}
+
+extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n,
+                                int d, int bits, int gs, int rb, float *y) {
+    const int wbits = bits == 0 ? 8 : bits, sf32 = bits == 0;
+    if (!w || !ws || !xq || !xs || !y || M < 1 || n <= 0 || d <= 0 || d % 4 || n % 16 ||
+        (bits != 0 && bits != 4 && bits != 8) || (gs != 32 && gs != 64) || (bits != 0 && gs != 32) || n % gs ||
+        (rb != 8 && rb != 16 && rb != 64)) {
+        fprintf(stderr, "mvh_prefill_gemm: bad arguments (M=%d n=%d d=%d bits=%d gs=%d rb=%d)\n", M, n, d, bits, gs, rb);
+        return -1;
+    }
+    if (hook_device("mvh_prefill_gemm")) return -1;
+    const int ng = n / gs;
+    TiledMat T = tiled_describe(d, n, gs, wbits, sf32, rb);
+    const size_t wbytes = (size_t)d * n * wbits / 8, sbytes = (size_t)d * ng * (sf32 ? 4 : 2);
+    uint8_t *dw = nullptr, *dsc = nullptr, *dt = nullptr;
+    int8_t *dx = nullptr;
+    float *dxs = nullptr, *dy = nullptr;
+    int *dmap = nullptr;
+    std::vector<int> map(d);
+    for (int i = 0; i < d; i++) map[i] = i;
+    int rc = -1;
+    if (hipMalloc(&dw, wbytes) == hipSuccess && hipMalloc(&dsc, sbytes) == hipSuccess &&
+        hipMalloc(&dt, T.bytes) == hipSuccess && hipMalloc(&dx, (size_t)M * n) == hipSuccess &&
+        hipMalloc(&dxs, (size_t)M * ng * 4) == hipSuccess && hipMalloc(&dy, (size_t)M * d * 4) == hipSuccess &&
+        hipMalloc(&dmap, (size_t)d * 4) == hipSuccess &&
+        hipMemcpy(dw, w, wbytes, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dsc, ws, sbytes, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dx, xq, (size_t)M * n, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dxs, xs, (size_t)M * ng * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dmap, map.data(), (size_t)d * 4, hipMemcpyHostToDevice) == hipSuccess) {
+        T.data = dt;
+        RepackArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.T = T;
+        ra.w[0] = dw;
+        ra.s[0] = dsc;
+        ra.rowmap = dmap;
+        PgemmArgs g;
+        memset(&g, 0, sizeof g);
+        g.W = T;
+        g.xq = dx;
+        g.xs = dxs;
+        g.y = dy;
+        g.M = M;
+        if (launch_repack(ra, 0) == hipSuccess && launch_pgemm(wbits, gs, sf32, g, 0) == hipSuccess &&
+            hipDeviceSynchronize() == hipSuccess &&
+            hipMemcpy(y, dy, (size_t)M * d * 4, hipMemcpyDeviceToHost) == hipSuccess)
+            rc = 0;
+    }
+    if (rc) fprintf(stderr, "mvh_prefill_gemm: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    hipFree(dw);
+    hipFree(dsc);
+    hipFree(dt);
+    hipFree(dx);
+    hipFree(dxs);
+    hipFree(dy);
     hipFree(dmap);
     return rc;
 }

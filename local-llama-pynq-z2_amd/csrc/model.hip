@@ -21,11 +21,13 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <string>
 #include <vector>
 
 #include "../../include/llm_hip.h"
 #include "host_common.h"
+#include "prefill.h"
 
 namespace {
 
@@ -70,6 +72,11 @@ struct llm_model {
     StepCtrl *ctrl = nullptr;
     int *prompt = nullptr, *tokens = nullptr, *gen = nullptr;
     hipGraphExec_t g_plain = nullptr, g_hist = nullptr;
+    // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
+    int pf_cap = 0, prefill_on = 1;
+    float *pf_x = nullptr, *pf_y = nullptr, *pf_q = nullptr, *pf_z = nullptr, *pf_s = nullptr;
+    int8_t *pf_a = nullptr;
+    int *pf_ids = nullptr;
     // file mapping during load
     const uint8_t *file = nullptr;
     size_t file_size = 0;
@@ -121,6 +128,18 @@ hipError_t launch_finalize(llm_model *m) {
     g.ctrl = m->ctrl;
     g.gen = m->gen;
     return launch_argmax(g, m->st);
+}
+
+// final rmsnorm + head GEMV of m->x (qwen.c:568-572): logits and per-block argmax partials
+hipError_t launch_head(llm_model *m, bool hist) {
+    GemvArgs a = base_args(m, m->head, m->s_head);
+    a.x = m->x;
+    a.norm_w = out_norm(m);
+    a.out = m->logits;
+    a.logits_hist = hist ? m->hist : nullptr;
+    a.part_val = m->part_v;
+    a.part_idx = m->part_i;
+    return launch_gemv(8, m->gs, m->head.sf32, PRO_NORM, EPI_ARGMAX, a, m->s_head.grid, m->st);
 }
 
 // Enqueue one decode step on m->st.  prof != NULL records events around every launch.
@@ -235,15 +254,8 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         done();
     }
 
-    GemvArgs a = base_args(m, m->head, m->s_head);
-    a.x = m->x;
-    a.norm_w = out_norm(m);
-    a.out = m->logits;
-    a.logits_hist = hist ? m->hist : nullptr;
-    a.part_val = m->part_v;
-    a.part_idx = m->part_i;
     mark(K_HEAD, gemv_algo_bytes(m->head.rows, dim, 8, m->gs, m->head.sf32));
-    HIP_OR_FAIL("llm", launch_gemv(8, m->gs, m->head.sf32, PRO_NORM, EPI_ARGMAX, a, m->s_head.grid, m->st));
+    HIP_OR_FAIL("llm", launch_head(m, hist));
     done();
 
     if (finalize) { // the step's own argmax; in a captured sequence the next step's start kernel does it
@@ -692,12 +704,124 @@ int load_bin(llm_model *m, const char *path) {
     return 0;
 }
 
+// ---- prefill (batched prompt processing)
+
+const int PREFILL_CHUNK = 512; // tokens per pass through the layers
+
+int prefill_alloc(llm_model *m, int M) {
+    if (M <= m->pf_cap) return 0;
+    const llm_info &I = m->info;
+    const int dim = I.dim, hid = I.hidden_dim, rows = std::max(dim + 2 * m->kv_dim, 2 * hid), wmax = std::max(dim, hid);
+    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
+                    (void *)m->pf_a, (void *)m->pf_ids})
+        if (p) hipFree(p);
+    m->pf_cap = 0;
+    if (hipMalloc(&m->pf_x, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_y, (size_t)M * rows * 4) != hipSuccess ||
+        hipMalloc(&m->pf_q, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_z, (size_t)M * dim * 4) != hipSuccess ||
+        hipMalloc(&m->pf_s, (size_t)M * (wmax / m->gs) * 4) != hipSuccess ||
+        hipMalloc(&m->pf_a, (size_t)M * wmax) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess) {
+        fprintf(stderr, "llm_prefill: cannot allocate the activations of %d tokens\n", M);
+        return -1;
+    }
+    m->pf_cap = M;
+    return 0;
+}
+
+// positions p0 .. p0 + M - 1 (token ids in host memory) through every layer; the residual stream of the chunk
+// is left in pf_x and its K/V rows in the caches
+int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
+    const llm_info &I = m->info;
+    const int dim = I.dim, kv = m->kv_dim, wb = m->kind == 0 ? 4 : 8, sf = m->kind == 0 ? 0 : 1;
+    HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->pf_ids, ids, (size_t)M * 4, hipMemcpyHostToDevice, m->st));
+    ProwArgs pa;
+    memset(&pa, 0, sizeof pa);
+    pa.M = M;
+    pa.p0 = p0;
+    pa.dim = dim;
+    pa.kv_dim = kv;
+    pa.head_size = m->hs;
+    pa.hidden = I.hidden_dim;
+    pa.gs = m->gs;
+    pa.qflavor = m->qflavor;
+    pa.rope_kind = m->kind == 0 ? ROPE_NEOX : ROPE_INTERLEAVED;
+    pa.eps = I.rms_eps;
+    pa.ids = m->pf_ids;
+    pa.emb_q = m->emb_q;
+    pa.emb_s = m->emb_s;
+    pa.emb_sf32 = m->emb_sf32;
+    pa.x = m->pf_x;
+    pa.y = m->pf_y;
+    pa.rope_cos = m->rope_cos;
+    pa.rope_sin = m->rope_sin;
+    pa.q = m->pf_q;
+    pa.oq = m->pf_a;
+    pa.os = m->pf_s;
+    pa.n_heads = I.n_heads;
+    pa.n_kv = I.n_kv_heads;
+    HIP_OR_FAIL("llm_prefill", launch_p_embed(pa, m->st));
+    PgemmArgs g;
+    memset(&g, 0, sizeof g);
+    g.xq = m->pf_a;
+    g.xs = m->pf_s;
+    g.y = m->pf_y;
+    g.M = M;
+    for (int l = 0; l < I.n_layers; l++) {
+        const Layer &Ly = m->L[l];
+        pa.kc = m->kc + (size_t)l * m->ctx * kv;
+        pa.vc = m->vc + (size_t)l * m->ctx * kv;
+        pa.bias = m->biases ? m->biases + (size_t)l * (dim + 2 * kv) : nullptr;
+        pa.norm_w = attn_norm(m, l);
+        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, m->st));
+        g.W = Ly.qkv;
+        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_qkv(pa, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_attention(pa, m->pf_z, m->st));
+        pa.z = m->pf_z;
+        pa.width = dim;
+        HIP_OR_FAIL("llm_prefill", launch_p_quant(pa, m->st));
+        g.W = Ly.o;
+        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
+        pa.norm_w = ffn_norm(m, l);
+        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, m->st));
+        g.W = Ly.gu;
+        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+        pa.gu_rb = Ly.gu.rb;
+        HIP_OR_FAIL("llm_prefill", launch_p_swiglu_quant(pa, m->st));
+        g.W = Ly.down;
+        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
+    }
+    return 0;
+}
+
+// All n prompt positions, then the head of the last one: logits, argmax partials, and (finalize) its argmax
+// into gen[n - 1].  Afterwards the step state is position n - 1, as after n forward() calls.
+int prefill_all(llm_model *m, const int *ids, int n) {
+    if (prefill_alloc(m, std::min(n, PREFILL_CHUNK))) return -1;
+    for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
+        const int M = std::min(PREFILL_CHUNK, n - p0);
+        if (prefill_chunk(m, ids + p0, p0, M)) return -1;
+        if (p0 + M == n)
+            HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * m->info.dim,
+                                                      (size_t)m->info.dim * 4, hipMemcpyDeviceToDevice, m->st));
+    }
+    HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->tokens, ids, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+    if (set_ctrl(m, n - 1, ids[n - 1], 0, 0)) return -1;
+    HIP_OR_FAIL("llm_prefill", launch_head(m, false));
+    HIP_OR_FAIL("llm_prefill", launch_finalize(m));
+    return 0;
+}
+
 void free_model(llm_model *m) {
     if (m->st) hipStreamSynchronize(m->st);
     if (m->g_plain) hipGraphExecDestroy(m->g_plain);
     if (m->g_hist) hipGraphExecDestroy(m->g_hist);
     for (void *p : m->allocs) hipFree(p);
     if (m->hist) hipFree(m->hist);
+    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
+                    (void *)m->pf_a, (void *)m->pf_ids})
+        if (p) hipFree(p);
     if (m->st) hipStreamDestroy(m->st);
     if (m->file) munmap((void *)m->file, m->file_size);
     delete m;
@@ -818,7 +942,13 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
     // positions: the prompt, then one per generated token, within the context
     const int last_pos = n_prompt - 1 + max_new - 1 < m->ctx - 1 ? n_prompt - 1 + max_new - 1 : m->ctx - 1;
     const double t0 = now_ms();
-    for (int p = 0; p < n_prompt; p++) HIP_OR_FAIL("llm_generate", hipGraphLaunch(*g, m->st));
+    if (m->prefill_on && !hist && n_prompt > 1) {
+        // the prompt in one batched pass; the first decode step then finishes its last position's argmax
+        if (prefill_all(m, prompt, n_prompt)) return -1;
+        if (set_ctrl(m, n_prompt - 1, prompt[n_prompt - 1], n_prompt, 1)) return -1;
+    } else {
+        for (int p = 0; p < n_prompt; p++) HIP_OR_FAIL("llm_generate", hipGraphLaunch(*g, m->st));
+    }
     HIP_OR_FAIL("llm_generate", hipStreamSynchronize(m->st));
     const double t1 = now_ms();
     std::vector<int> gen(m->ctx);
@@ -948,10 +1078,27 @@ extern "C" int llm_read_state(llm_model *m, int which, int layer, float *dst, si
 }
 
 extern "C" int llm_prefill(llm_model *m, const int *ids, int n, float *logits) {
-    // batched prefill is not built yet: positions run one by one through the decode step
-    if (!m || !ids || n < 1 || n > m->ctx) return -1;
-    for (int p = 0; p < n; p++)
-        if (llm_forward(m, ids[p], p, p == n - 1 ? logits : nullptr)) return -1;
+    if (!m || !ids || n < 1 || n > m->ctx) {
+        fprintf(stderr, "llm_prefill: bad arguments\n");
+        return -1;
+    }
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->info.vocab_size) {
+            fprintf(stderr, "llm_prefill: token id %d out of range\n", ids[i]);
+            return -1;
+        }
+    hipSetDevice(m->device);
+    if (prefill_all(m, ids, n)) return -1;
+    if (logits)
+        HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(logits, m->logits, (size_t)m->info.n_logits * 4,
+                                                  hipMemcpyDeviceToHost, m->st));
+    HIP_OR_FAIL("llm_prefill", hipStreamSynchronize(m->st));
+    return 0;
+}
+
+extern "C" int llm_set_prefill(llm_model *m, int on) {
+    if (!m) return -1;
+    m->prefill_on = on != 0;
     return 0;
 }
 

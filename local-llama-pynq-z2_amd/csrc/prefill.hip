@@ -1,0 +1,310 @@
+// Prefill kernels of libmatvec_hip.so for gfx950: the prompt's positions through a layer together.
+//
+// The reference processes a prompt one position at a time with the same forward() (qwen.c:674-681); no
+// batched prefill exists there (README.md:386-387).  Here the M positions of a chunk share each weight
+// read: the layer matrices become int8 MFMA GEMMs (v_mfma_i32_32x32x32_i8) over the tiled records the decode
+// GEMV reads, with the per-group int32 sums exact and the group terms p = ((float)ival * ws) * xs added in
+// group order, which is the reference's matmul (qwen.c:436-456, runq.c:429-458) for every (row, token).
+// The element-wise steps of forward() run per token, and attention is causal over the KV cache.
+#include "attn.h"
+#include "prefill.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------------------------------------------------
+// GEMM: y[m][r] = sum_g ((float)ival(r, m, g) * ws[r][g]) * xs[m][g], groups in order.
+//
+// One wave per 32 rows x 32 tokens.  v_mfma_i32_32x32x32_i8 lane layout: A (rows x K): lane l holds row l%32,
+// K = 16 (l/32) .. +16; B (K x tokens): token l%32, same K half; D: token l%32, rows 8i + 4 (l/32) + j in
+// d[4i + j].  int4 weights enter as 16 * q (the nibble at the top of its byte, as in the GEMV), so D holds
+// 16 * ival; their fp16 scales are taken as ws / 16, an exact power-of-two step, and (16 ival) * (ws / 16)
+// rounds to the same float as ival * ws.
+//
+// Blocks are laid out so that all token tiles of one row tile run on the same XCD (block b goes to XCD b % 8):
+// each weight tile is read from HBM once and served from that XCD's L2 to its other token tiles.
+
+template <int WB, int GSZ, int SF32>
+__global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
+    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32;
+    const TiledMat &W = a.W;
+    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
+    // block -> (row tile, token tile): XCD j = b % 8 takes row tiles j, j + 8, ...
+    const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
+    const int tx = xcd + 8 * (idx / yt), ty = idx - (idx / yt) * yt;
+    if (tx >= xt) return;
+    const int l = threadIdx.x, h = l >> 5, rl = l & 31;
+    const int r0 = tx * 32, m0 = ty * 32;
+    const int rb = W.rb, gpc = WAVE / rb, n = W.n, ng = W.ng;
+    const int rowA = min(r0 + rl, W.rows - 1), tok = min(m0 + rl, a.M - 1);
+    const int bA = rowA / rb, laneA = rowA - bA * rb; // + gi * rb per group
+    // scale rows r0 + 8i + 4h .. +3: four rows of one row-block, contiguous in the record's scale area
+    int bS[4], laneS[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int R4 = min(r0 + 8 * i + 4 * h, W.rows - 4);
+        bS[i] = R4 / rb;
+        laneS[i] = R4 - bS[i] * rb;
+    }
+    const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
+    const float *xsrow = a.xs + (size_t)tok * ng;
+
+    v4i av[2][KC], bv[2][KC];
+    float ws[2][16], xs[2];
+    auto load = [&](int g, int s) {
+        const int c = g / gpc, gi = g - c * gpc;
+        const uint8_t *recA = W.data + ((size_t)bA * W.nchunks + c) * W.rec;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            if constexpr (WB == 4) {
+                const uint4 w = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
+                const uint32_t m = 0xF0F0F0F0u;
+                if (h == 0) av[s][kc] = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m),
+                                            (int)((w.w << 4) & m)};
+                else av[s][kc] = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
+            } else {
+                av[s][kc] = *(const v4i *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
+            }
+            bv[s][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint8_t *sp = W.data + ((size_t)bS[i] * W.nchunks + c) * W.rec + 64 * SB + (size_t)(gi * rb + laneS[i]) * SCB;
+            if constexpr (SF32) {
+                const float4 f = *(const float4 *)sp;
+                ws[s][4 * i] = f.x;
+                ws[s][4 * i + 1] = f.y;
+                ws[s][4 * i + 2] = f.z;
+                ws[s][4 * i + 3] = f.w;
+            } else {
+                const uint2 u = *(const uint2 *)sp;
+                const float k = WB == 4 ? 0.0625f : 1.0f;
+                ws[s][4 * i] = f16_bits_to_f32((uint16_t)(u.x & 0xffff)) * k;
+                ws[s][4 * i + 1] = f16_bits_to_f32((uint16_t)(u.x >> 16)) * k;
+                ws[s][4 * i + 2] = f16_bits_to_f32((uint16_t)(u.y & 0xffff)) * k;
+                ws[s][4 * i + 3] = f16_bits_to_f32((uint16_t)(u.y >> 16)) * k;
+            }
+        }
+        xs[s] = xsrow[g];
+    };
+    float acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc[k] = 0.0f;
+    auto compute = [&](int s) {
+        v16i d = {};
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s][kc], bv[s][kc], d, 0, 0, 0);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            float p = (float)d[k] * ws[s][k]; // qwen.c:452, runq.c:452
+            p = p * xs[s];
+            acc[k] = acc[k] + p;
+        }
+    };
+    load(0, 0);
+    for (int g = 0; g < ng; g += 2) {
+        if (g + 1 < ng) load(g + 1, 1);
+        compute(0);
+        if (g + 1 >= ng) break;
+        if (g + 2 < ng) load(g + 2, 0);
+        compute(1);
+    }
+    const int m = m0 + rl;
+    if (m < a.M) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int R = r0 + 8 * i + 4 * h;
+            float *dst = a.y + (size_t)m * W.rows + R;
+            if (R + 3 < W.rows) *(float4 *)dst = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
+            else
+                for (int j = 0; j < 4; j++)
+                    if (R + j < W.rows) dst[j] = acc[4 * i + j];
+        }
+    }
+}
+
+hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStream_t st) {
+    const TiledMat &W = a.W;
+    // rows in whole groups of 4 (scale loads), 16-byte aligned activation rows and output rows
+    if (a.M < 1 || W.rows % 4 || W.n % gs || W.n % 16 || ((uintptr_t)a.xq & 15) || ((uintptr_t)a.y & 15) ||
+        W.gs != gs || W.wbits != wbits || W.sf32 != sf32)
+        return hipErrorInvalidValue;
+    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
+    const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * yt);
+#define PG(WB_, GS_, SF_)                                                                                      \
+    if (wbits == WB_ && gs == GS_ && sf32 == SF_) {                                                           \
+        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_>), dim3(blocks), dim3(64), 0, st, a);                       \
+        return hipGetLastError();                                                                             \
+    }
+    PG(4, 32, 0)
+    PG(8, 32, 0)
+    PG(8, 32, 1)
+    PG(8, 64, 1)
+#undef PG
+    return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------------------------------------------
+// per-token element-wise steps (one block of 256 threads per token)
+
+// embedding rows (qwen.c:498-501, runq.c:490-492)
+__global__ void __launch_bounds__(256) k_p_embed(ProwArgs a) {
+    const int m = blockIdx.x, token = a.ids[m], ngr = a.dim / a.gs;
+    const int8_t *er = a.emb_q + (size_t)token * a.dim;
+    for (int i = threadIdx.x; i < a.dim; i += blockDim.x) {
+        const int g = i / a.gs;
+        const float sc = a.emb_sf32 ? ((const float *)a.emb_s)[(size_t)token * ngr + g]
+                                    : f16_bits_to_f32(((const uint16_t *)a.emb_s)[(size_t)token * ngr + g]);
+        a.x[(size_t)m * a.dim + i] = (float)er[i] * sc;
+    }
+}
+
+// rmsnorm (qwen.c:337-344, runq.c:394-407) of x[m], then int8 quantization (qwen.c:354-364 / runq.c:244-270)
+__global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
+    extern __shared__ __align__(16) float sv[]; // dim floats + 4 per wave
+    const int m = blockIdx.x, n = a.dim;
+    const float *x = a.x + (size_t)m * n;
+    float part = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        sv[i] = v;
+        part += v * v;
+    }
+    float ss = block_sum(part, sv + n);
+    ss /= (float)n;
+    ss += a.eps;
+    ss = 1.0f / sqrtf(ss);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.norm_w[i] * (ss * sv[i]);
+    __syncthreads();
+    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
+}
+
+// int8 quantization of z[m] (the attention output, qwen.c:549 / runq.c:571)
+__global__ void __launch_bounds__(256) k_p_quant(ProwArgs a) {
+    extern __shared__ __align__(16) float sv[];
+    const int m = blockIdx.x, n = a.width;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.z[(size_t)m * n + i];
+    __syncthreads();
+    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
+}
+
+// QKV rows of token m: bias (qwen.c:521-522), RoPE at position p0 + m (qwen.c:478-488 NeoX pairs; runq.c:506-521
+// interleaved pairs), q to q[m], k and v into the caches.  Logical rows follow the fused matrix's order.
+__global__ void __launch_bounds__(256) k_p_qkv(ProwArgs a) {
+    const int m = blockIdx.x, pos = a.p0 + m, dim = a.dim, kvd = a.kv_dim, hs = a.head_size, half = hs / 2;
+    const int rows = dim + 2 * kvd;
+    const float *y = a.y + (size_t)m * rows;
+    for (int R = threadIdx.x; R < rows; R += blockDim.x) {
+        const float v = y[R];
+        if (a.rope_kind == ROPE_NEOX) {
+            if (R < dim + kvd) {
+                const int blk = R / 16, r = R & 15, per = half / 8, hh = blk / per, i = (blk - hh * per) * 8 + (r & 7);
+                const bool first = r < 8;
+                const int e = hh * hs + (first ? i : half + i), ep = hh * hs + (first ? half + i : i);
+                const float c = a.rope_cos[(size_t)pos * half + i], sn = a.rope_sin[(size_t)pos * half + i];
+                const float self = v + a.bias[e], partner = y[R ^ 8] + a.bias[ep];
+                float o;
+                if (first) { float t1 = self * c, t2 = partner * sn; o = t1 - t2; }
+                else { float t1 = self * c, t2 = partner * sn; o = t1 + t2; }
+                if (e < dim) a.q[(size_t)m * dim + e] = o;
+                else a.kc[(size_t)pos * kvd + (e - dim)] = o;
+            } else {
+                a.vc[(size_t)pos * kvd + (R - dim - kvd)] = v + a.bias[R];
+            }
+        } else {
+            if (R < dim + kvd) {
+                const int e = R < dim ? R : R - dim, i = (e % hs) / 2;
+                const float c = a.rope_cos[(size_t)pos * half + i], sn = a.rope_sin[(size_t)pos * half + i];
+                const float partner = y[R ^ 1];
+                float o;
+                if ((e & 1) == 0) { float t1 = v * c, t2 = partner * sn; o = t1 - t2; }
+                else { float t1 = partner * sn, t2 = v * c; o = t1 + t2; }
+                if (R < dim) a.q[(size_t)m * dim + e] = o;
+                else a.kc[(size_t)pos * kvd + e] = o;
+            } else {
+                a.vc[(size_t)pos * kvd + (R - dim - kvd)] = v;
+            }
+        }
+    }
+}
+
+// x += y (qwen.c:551, 565; runq.c:575-577, 603-605)
+__global__ void __launch_bounds__(256) k_p_resid(ProwArgs a) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, total = (size_t)a.M * a.dim;
+    if (i < total) a.x[i] = a.x[i] + a.y[i];
+}
+
+// SwiGLU of token m (qwen.c:556-562, runq.c:589-596), then int8 quantization of h.  The gate/up matrix's rows
+// come in row-blocks of gu_rb: gu_rb/2 gate rows, then the matching up rows.
+__global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
+    extern __shared__ __align__(16) float sv[];
+    const int m = blockIdx.x, hid = a.hidden, hb = a.gu_rb / 2;
+    const float *y = a.y + (size_t)m * 2 * hid;
+    for (int j = threadIdx.x; j < hid; j += blockDim.x) {
+        const int b = j / hb, r = j - b * hb;
+        float g = y[b * a.gu_rb + r];
+        const float u = y[b * a.gu_rb + hb + r];
+        const float sig = 1.0f / (1.0f + expf(-g));
+        g = g * sig;
+        sv[j] = g * u;
+    }
+    __syncthreads();
+    block_quantize(sv, hid, a.gs, a.qflavor, a.oq + (size_t)m * hid, a.os + (size_t)m * (hid / a.gs));
+}
+
+// causal attention of token m (positions 0 .. p0 + m), block = (kv head, token); out[m] = acc / sum
+__global__ void __launch_bounds__(256) k_p_attention(ProwArgs a, float *out) {
+    extern __shared__ __align__(16) float sm[];
+    const int kvh = blockIdx.x, m = blockIdx.y, hs = a.head_size, kv_mul = a.n_heads / a.n_kv, dim = a.dim;
+    float acc[4];
+    const float *ml_max, *ml_sum;
+    attn_range(a.q + (size_t)m * dim + (size_t)kvh * kv_mul * hs, a.kc, a.vc, a.kv_dim, kvh, hs, kv_mul, 0,
+               a.p0 + m + 1, sm, acc, &ml_max, &ml_sum);
+    const int n_out = kv_mul * hs;
+    for (int k = 0; k < 4; k++) {
+        const int o = threadIdx.x + k * blockDim.x;
+        if (o < n_out) {
+            const int j = o / hs;
+            out[(size_t)m * dim + (size_t)kvh * n_out + o] = acc[k] / ml_sum[j];
+        }
+    }
+}
+
+hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_p_embed, dim3(a.M), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_norm_quant(const ProwArgs &a, hipStream_t st) {
+    if (a.dim % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_p_norm_quant, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st) {
+    if (a.width % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_p_quant, dim3(a.M), dim3(256), (size_t)a.width * 4, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st) {
+    if (a.rope_kind == ROPE_NEOX && !a.bias) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_p_qkv, dim3(a.M), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_resid(const ProwArgs &a, hipStream_t st) {
+    const size_t total = (size_t)a.M * a.dim;
+    hipLaunchKernelGGL(k_p_resid, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st) {
+    if (a.hidden % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_p_swiglu_quant, dim3(a.M), dim3(256), (size_t)a.hidden * 4, st, a);
+    return hipGetLastError();
+}
+hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st) {
+    const int kv_mul = a.n_heads / a.n_kv;
+    if (kv_mul * a.head_size > 1024 || a.head_size % 4 || a.head_size > 128 || ((uintptr_t)a.q & 15) ||
+        ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) || a.kv_dim % 4 || a.dim % 4)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M), dim3(256), attn_lds_floats(kv_mul, a.head_size) * 4, st, a,
+                       out);
+    return hipGetLastError();
+}
