@@ -75,6 +75,7 @@ struct llm_model {
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, prefill_on = 1;
     float *pf_x = nullptr, *pf_y = nullptr, *pf_q = nullptr, *pf_z = nullptr, *pf_s = nullptr;
+    float *pf_ml = nullptr, *pf_acc = nullptr; // attention slice partials
     int8_t *pf_a = nullptr;
     int *pf_ids = nullptr;
     // file mapping during load
@@ -713,13 +714,15 @@ int prefill_alloc(llm_model *m, int M) {
     const llm_info &I = m->info;
     const int dim = I.dim, hid = I.hidden_dim, rows = std::max(dim + 2 * m->kv_dim, 2 * hid), wmax = std::max(dim, hid);
     for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
-                    (void *)m->pf_a, (void *)m->pf_ids})
+                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
         if (p) hipFree(p);
     m->pf_cap = 0;
     if (hipMalloc(&m->pf_x, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_y, (size_t)M * rows * 4) != hipSuccess ||
         hipMalloc(&m->pf_q, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_z, (size_t)M * dim * 4) != hipSuccess ||
         hipMalloc(&m->pf_s, (size_t)M * (wmax / m->gs) * 4) != hipSuccess ||
-        hipMalloc(&m->pf_a, (size_t)M * wmax) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess) {
+        hipMalloc(&m->pf_a, (size_t)M * wmax) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess ||
+        hipMalloc(&m->pf_ml, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * 2 * 4) != hipSuccess ||
+        hipMalloc(&m->pf_acc, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * m->hs * 4) != hipSuccess) {
         fprintf(stderr, "llm_prefill: cannot allocate the activations of %d tokens\n", M);
         return -1;
     }
@@ -758,6 +761,9 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     pa.os = m->pf_s;
     pa.n_heads = I.n_heads;
     pa.n_kv = I.n_kv_heads;
+    prefill_att_slices(p0 + M, &pa.att_sl, &pa.att_smax);
+    pa.att_ml = m->pf_ml;
+    pa.att_acc = m->pf_acc;
     HIP_OR_FAIL("llm_prefill", launch_p_embed(pa, m->st));
     PgemmArgs g;
     memset(&g, 0, sizeof g);
@@ -820,7 +826,7 @@ void free_model(llm_model *m) {
     for (void *p : m->allocs) hipFree(p);
     if (m->hist) hipFree(m->hist);
     for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
-                    (void *)m->pf_a, (void *)m->pf_ids})
+                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
         if (p) hipFree(p);
     if (m->st) hipStreamDestroy(m->st);
     if (m->file) munmap((void *)m->file, m->file_size);

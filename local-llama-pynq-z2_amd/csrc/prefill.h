@@ -37,7 +37,21 @@ struct ProwArgs {           // per-token elementwise kernels
     float *os;              // [M][width / gs]
     int width;              // row width of z / oq for k_p_quant
     int n_heads, n_kv;
+    // attention slices: positions of token m in slices of att_sl, at most att_smax per token; partials
+    // ml [M][n_heads][att_smax][2] (max, sum of exp) and acc [M][n_heads][att_smax][hs]
+    int att_sl, att_smax;
+    float *att_ml, *att_acc;
 };
+
+// Slices of at least 64 positions, at most 16 per token for a chunk ending at position `end`.
+static inline void prefill_att_slices(int end, int *sl, int *smax) {
+    int s = (end + 15) / 16;
+    if (s < 64) s = 64;
+    s = (s + 31) / 32 * 32;
+    *sl = s;
+    *smax = (end + s - 1) / s;
+}
+#define PREFILL_ATT_SMAX 16
 
 hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStream_t st);
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st);
@@ -46,4 +60,4 @@ hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_resid(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st);
-hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st);
+hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st); // slices, then their merge

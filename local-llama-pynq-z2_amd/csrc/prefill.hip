@@ -12,6 +12,9 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
+// groups of the prefill GEMM's K loop whose loads are in flight at once
+#define PF_STAGES 4
+
 // ------------------------------------------------------------------------------------------------------
 // GEMM: y[m][r] = sum_g ((float)ival(r, m, g) * ws[r][g]) * xs[m][g], groups in order.
 //
@@ -49,65 +52,80 @@ __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
     const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
     const float *xsrow = a.xs + (size_t)tok * ng;
 
-    v4i av[2][KC], bv[2][KC];
-    float ws[2][16], xs[2];
-    auto load = [&](int g, int s) {
+    // A ring of PF_STAGES groups in flight.  A stage holds raw loaded words only: the int4 unpacking and the
+    // scale conversion happen when the group is used, so issuing a stage never waits for its loads.
+    constexpr int NS = PF_STAGES, SCW = SF32 ? 4 : 2; // SCW: 32-bit words of one row quad's scales
+    uint4 wr[NS][KC];                                 // int4: the lane's 16-byte segment; int8: the K-half piece
+    v4i bv[NS][KC];
+    uint32_t sr[NS][4][SCW];
+    float xs[NS];
+    auto load = [&](int g, int st) {
         const int c = g / gpc, gi = g - c * gpc;
         const uint8_t *recA = W.data + ((size_t)bA * W.nchunks + c) * W.rec;
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) {
-            if constexpr (WB == 4) {
-                const uint4 w = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
-                const uint32_t m = 0xF0F0F0F0u;
-                if (h == 0) av[s][kc] = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m),
-                                            (int)((w.w << 4) & m)};
-                else av[s][kc] = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
-            } else {
-                av[s][kc] = *(const v4i *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
-            }
-            bv[s][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
+            if constexpr (WB == 4) wr[st][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
+            else wr[st][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
+            bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint8_t *sp = W.data + ((size_t)bS[i] * W.nchunks + c) * W.rec + 64 * SB + (size_t)(gi * rb + laneS[i]) * SCB;
             if constexpr (SF32) {
-                const float4 f = *(const float4 *)sp;
-                ws[s][4 * i] = f.x;
-                ws[s][4 * i + 1] = f.y;
-                ws[s][4 * i + 2] = f.z;
-                ws[s][4 * i + 3] = f.w;
+                const uint4 u = *(const uint4 *)sp;
+                sr[st][i][0] = u.x;
+                sr[st][i][1] = u.y;
+                sr[st][i][2] = u.z;
+                sr[st][i][3] = u.w;
             } else {
                 const uint2 u = *(const uint2 *)sp;
-                const float k = WB == 4 ? 0.0625f : 1.0f;
-                ws[s][4 * i] = f16_bits_to_f32((uint16_t)(u.x & 0xffff)) * k;
-                ws[s][4 * i + 1] = f16_bits_to_f32((uint16_t)(u.x >> 16)) * k;
-                ws[s][4 * i + 2] = f16_bits_to_f32((uint16_t)(u.y & 0xffff)) * k;
-                ws[s][4 * i + 3] = f16_bits_to_f32((uint16_t)(u.y >> 16)) * k;
+                sr[st][i][0] = u.x;
+                sr[st][i][1] = u.y;
             }
         }
-        xs[s] = xsrow[g];
+        xs[st] = xsrow[g];
     };
     float acc[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) acc[k] = 0.0f;
-    auto compute = [&](int s) {
+    auto compute = [&](int st) {
         v16i d = {};
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[s][kc], bv[s][kc], d, 0, 0, 0);
-#pragma unroll
-        for (int k = 0; k < 16; k++) {
-            float p = (float)d[k] * ws[s][k]; // qwen.c:452, runq.c:452
-            p = p * xs[s];
-            acc[k] = acc[k] + p;
+        for (int kc = 0; kc < KC; kc++) {
+            v4i av;
+            if constexpr (WB == 4) {
+                const uint4 w = wr[st][kc];
+                const uint32_t m = 0xF0F0F0F0u;
+                if (h == 0) av = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m), (int)((w.w << 4) & m)};
+                else av = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
+            } else {
+                av = v4i{(int)wr[st][kc].x, (int)wr[st][kc].y, (int)wr[st][kc].z, (int)wr[st][kc].w};
+            }
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d, 0, 0, 0);
         }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float ws;
+                if constexpr (SF32) ws = __uint_as_float(sr[st][i][j]);
+                else ws = f16_bits_to_f32((uint16_t)(sr[st][i][j >> 1] >> (16 * (j & 1)))) * (WB == 4 ? 0.0625f : 1.0f);
+                float p = (float)d[4 * i + j] * ws; // qwen.c:452, runq.c:452
+                p = p * xs[st];
+                acc[4 * i + j] = acc[4 * i + j] + p;
+            }
     };
-    load(0, 0);
-    for (int g = 0; g < ng; g += 2) {
-        if (g + 1 < ng) load(g + 1, 1);
-        compute(0);
-        if (g + 1 >= ng) break;
-        if (g + 2 < ng) load(g + 2, 0);
-        compute(1);
+#pragma unroll
+    for (int st = 0; st < NS - 1; st++)
+        if (st < ng) load(st, st);
+    for (int g0 = 0; g0 < ng; g0 += NS) {
+#pragma unroll
+        for (int st = 0; st < NS; st++) {
+            const int g = g0 + st;
+            if (g >= ng) break;
+            if (g + NS - 1 < ng) load(g + NS - 1, (st + NS - 1) % NS);
+            compute(st);
+        }
     }
     const int m = m0 + rl;
     if (m < a.M) {
@@ -252,21 +270,49 @@ __global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
     block_quantize(sv, hid, a.gs, a.qflavor, a.oq + (size_t)m * hid, a.os + (size_t)m * (hid / a.gs));
 }
 
-// causal attention of token m (positions 0 .. p0 + m), block = (kv head, token); out[m] = acc / sum
-__global__ void __launch_bounds__(256) k_p_attention(ProwArgs a, float *out) {
+// causal attention of token m over positions 0 .. p0 + m, cut into slices of att_sl positions: block =
+// (kv head, token, slice) leaves the slice's running max, sum of exponentials and exp-weighted value sums
+__global__ void __launch_bounds__(256) k_p_attention(ProwArgs a) {
     extern __shared__ __align__(16) float sm[];
-    const int kvh = blockIdx.x, m = blockIdx.y, hs = a.head_size, kv_mul = a.n_heads / a.n_kv, dim = a.dim;
+    const int kvh = blockIdx.x, m = blockIdx.y, s = blockIdx.z, hs = a.head_size, kv_mul = a.n_heads / a.n_kv;
+    const int t_begin = s * a.att_sl, t_end = min(t_begin + a.att_sl, a.p0 + m + 1);
+    if (t_begin >= t_end) return;
     float acc[4];
     const float *ml_max, *ml_sum;
-    attn_range(a.q + (size_t)m * dim + (size_t)kvh * kv_mul * hs, a.kc, a.vc, a.kv_dim, kvh, hs, kv_mul, 0,
-               a.p0 + m + 1, sm, acc, &ml_max, &ml_sum);
+    attn_range(a.q + (size_t)m * a.dim + (size_t)kvh * kv_mul * hs, a.kc, a.vc, a.kv_dim, kvh, hs, kv_mul, t_begin,
+               t_end, sm, acc, &ml_max, &ml_sum);
     const int n_out = kv_mul * hs;
     for (int k = 0; k < 4; k++) {
         const int o = threadIdx.x + k * blockDim.x;
         if (o < n_out) {
-            const int j = o / hs;
-            out[(size_t)m * dim + (size_t)kvh * n_out + o] = acc[k] / ml_sum[j];
+            const int j = o / hs, e = o - j * hs, h = kvh * kv_mul + j;
+            a.att_acc[(((size_t)m * a.n_heads + h) * a.att_smax + s) * hs + e] = acc[k];
         }
+    }
+    if (threadIdx.x < kv_mul) {
+        const int h = kvh * kv_mul + threadIdx.x;
+        float *ml = a.att_ml + (((size_t)m * a.n_heads + h) * a.att_smax + s) * 2;
+        ml[0] = ml_max[threadIdx.x];
+        ml[1] = ml_sum[threadIdx.x];
+    }
+}
+
+// merge of token m's slices: out[m][h*hs + e] = sum_s acc_s[e] * exp(max_s - max) / sum_s l_s * exp(max_s - max)
+__global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, float *out) {
+    const int m = blockIdx.x, hs = a.head_size, S = (a.p0 + m + a.att_sl) / a.att_sl;
+    for (int o = threadIdx.x; o < a.dim; o += blockDim.x) {
+        const int h = o / hs, e = o - h * hs;
+        const float *ml = a.att_ml + ((size_t)m * a.n_heads + h) * a.att_smax * 2;
+        const float *acc = a.att_acc + ((size_t)m * a.n_heads + h) * a.att_smax * hs + e;
+        float mx = ml[0];
+        for (int k = 1; k < S; k++) mx = fmaxf(mx, ml[2 * k]);
+        float l = 0.0f, v = 0.0f;
+        for (int k = 0; k < S; k++) {
+            const float f = expf(ml[2 * k] - mx);
+            l += ml[2 * k + 1] * f;
+            v += acc[(size_t)k * hs] * f;
+        }
+        out[(size_t)m * a.dim + o] = v / l;
     }
 }
 
@@ -302,9 +348,13 @@ hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st) {
 hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv;
     if (kv_mul * a.head_size > 1024 || a.head_size % 4 || a.head_size > 128 || ((uintptr_t)a.q & 15) ||
-        ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) || a.kv_dim % 4 || a.dim % 4)
+        ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) || a.kv_dim % 4 || a.dim % 4 || a.att_sl < ATT_SUB ||
+        a.att_smax < 1 || a.att_smax > PREFILL_ATT_SMAX || (a.p0 + a.M + a.att_sl - 1) / a.att_sl > a.att_smax)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M), dim3(256), attn_lds_floats(kv_mul, a.head_size) * 4, st, a,
-                       out);
+    hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M, a.att_smax), dim3(256),
+                       attn_lds_floats(kv_mul, a.head_size) * 4, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_p_attn_merge, dim3(a.M), dim3(256), 0, st, a, out);
     return hipGetLastError();
 }
