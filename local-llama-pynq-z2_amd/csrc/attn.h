@@ -83,11 +83,18 @@ __device__ __forceinline__ void attn_range(const float *q, const float *kc, cons
         __syncthreads();
         KERNEL_MARK(2);
         if (t0 + ATT_SUB < t_end) load_kv(t0 + ATT_SUB);
-        for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), i in order
+        for (int i = tid; i < kv_mul * T; i += nt) { // score = (q . k) / sqrtf(hs), e in order
             const int j = i / T, t = i - j * T;
-            const float *qq = sq + j * hs, *kk = sk + t * ks;
+            const f32x4 *qq = (const f32x4 *)(sq + j * hs), *kk = (const f32x4 *)(sk + t * ks);
             float d = 0.0f;
-            for (int e = 0; e < hs; e++) d += qq[e] * kk[e];
+#pragma unroll 4
+            for (int e4 = 0; e4 < hs4; e4++) {
+                const f32x4 a4 = qq[e4], b4 = kk[e4];
+                d += a4.x * b4.x;
+                d += a4.y * b4.y;
+                d += a4.z * b4.z;
+                d += a4.w * b4.w;
+            }
             sc[j * ATT_SUB + t] = d / rs;
         }
         __syncthreads();
@@ -113,7 +120,9 @@ __device__ __forceinline__ void attn_range(const float *q, const float *kc, cons
             if (o < n_out) {
                 const int j = o / hs, e = o - j * hs;
                 float v = acc[k] * sf[j];
-                for (int t = 0; t < T; t++) v += sc[j * ATT_SUB + t] * sv[t * hs + e];
+                const float *sj = sc + j * ATT_SUB, *se = sv + e;
+#pragma unroll 8
+                for (int t = 0; t < T; t++) v += sj[t] * se[t * hs];
                 acc[k] = v;
             }
         }

@@ -39,7 +39,10 @@ enum { ROPE_NEOX = 0, ROPE_INTERLEAVED = 1 };
 
 struct GemvArgs {
     TiledMat W;
-    int kw, nb;             // waves per row-block, row-blocks per block iteration
+    int kw, nb;             // waves per row-block, row-blocks per block iteration (a power of two)
+    // derived by launch_gemv: log2(nb), log2(W.rb), iterations, chunks per wave (kw_base + (my_kw < kw_rem)),
+    // iterations per block (it_base + (block < it_rem))
+    int nb_log2, rb_log2, n_it, kw_base, kw_rem, it_base, it_rem;
     int qflavor;            // activation quantization flavour (QF_QWEN / QF_RUNQ)
     const StepCtrl *ctrl;
     // PRO_XQ

@@ -81,8 +81,16 @@ __device__ __forceinline__ float rope_pair_out(float self, float partner, bool f
     return t1 + t2;
 }
 
+// Weights are read through a buffer resource: the record's byte offset is a scalar, the lane's position in the
+// record a per-lane constant, so a chunk costs one scalar multiply-add of address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const TiledMat &W) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)W.data, 0, (int)(W.bytes < 0x7fffffffu ? W.bytes : 0x7fffffffu),
+                                            0x00020000);
+}
+
 template <int WB, int GSZ, int SF32>
-__device__ __forceinline__ void load_batch(const uint8_t *base, size_t rec_bytes, int nchunks, int c0, int kw, int lane,
+__device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, uint32_t rb_off, uint32_t rec_bytes, int nchunks,
+                                           int c0, int kw, int lane,
                                            uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
                                            uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
     using F = Fmt<WB, GSZ, SF32>;
@@ -90,12 +98,14 @@ __device__ __forceinline__ void load_batch(const uint8_t *base, size_t rec_bytes
     // then skips.  Unconditional loads keep the wave from waiting for them at a branch merge.
 #pragma unroll
     for (int u = 0; u < F::UNROLL; u++) {
-        const int c = min(c0 + u * kw, nchunks - 1);
-        const uint8_t *rec = base + (size_t)c * rec_bytes;
+        const uint32_t soff = rb_off + (uint32_t)min(c0 + u * kw, nchunks - 1) * rec_bytes;
 #pragma unroll
-        for (int p = 0; p < F::PIECES; p++) wv[u][p] = *(const uint4 *)(rec + p * 1024 + lane * 16);
-        if constexpr (SF32) sr[u] = *(const uint32_t *)(rec + 64 * F::SB + lane * 4);
-        else sr[u] = *(const uint16_t *)(rec + 64 * F::SB + lane * 2);
+        for (int p = 0; p < F::PIECES; p++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + p * 1024, soff, 0);
+            wv[u][p] = *(const uint4 *)&v;
+        }
+        if constexpr (SF32) sr[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 64 * F::SB + lane * 4, soff, 0);
+        else sr[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 64 * F::SB + lane * 2, soff, 0);
     }
 }
 
@@ -173,10 +183,11 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     float *sred = sxs + ngp4;                             // nw * 64
     float *srow = sred + nw * WAVE;                       // nb * rb
     float *sv = srow + a.nb * rb;                         // prologue / epilogue floats
-    const int my_nb = wave / a.kw, my_kw = wave - my_nb * a.kw;
+    // wave = my_kw * nb + my_nb (nb a power of two); the launcher precomputes every quotient the shape needs
+    const int my_nb = wave & (a.nb - 1), my_kw = wave >> a.nb_log2;
     const int rows_it = a.nb * rb;
-    const int n_it = (W.nblocks + a.nb - 1) / a.nb;
-    const int g_lane = lane / rb;
+    const int n_it = a.n_it;
+    const int g_lane = lane >> a.rb_log2;
     const int it0 = blockIdx.x;
     KERNEL_MARK(0);
     const bool need_pos = PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX;
@@ -225,16 +236,18 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     // (2) the wave's first two weight batches.  The batches of all the block's iterations (it0, it0 + grid,
     // ...) form one stream per wave: bpi batches per iteration, two buffers, and the next iteration's first
     // batch is in flight while the current one is reduced and finished.
-    const int cnt_w = (W.nchunks - my_kw + a.kw - 1) / a.kw;     // chunks of a row-block for this wave (>= 1)
+    const int cnt_w = a.kw_base + (my_kw < a.kw_rem);           // chunks of a row-block for this wave (>= 1)
     const int bpi = (cnt_w + F::UNROLL - 1) / F::UNROLL;         // batches per iteration
-    const int n_my = it0 < n_it ? (n_it - 1 - it0) / (int)gridDim.x + 1 : 0;
+    const int n_my = a.it_base + (it0 < a.it_rem);               // iterations it0, it0 + grid, ... < n_it
     const int total = n_my * bpi;
     float pre_x = 0.0f, pre_x_next = 0.0f; // EPI_RESID: out[R] of this / the next iteration's row
     int iss_it = it0, iss_bi = 0;          // the next batch to issue
+    const __amdgpu_buffer_rsrc_t wrs = weight_rsrc(W);
+    const uint32_t rec = (uint32_t)W.rec, rb_bytes = (uint32_t)W.nchunks * rec;
     auto issue = [&](uint4 (&w)[F::UNROLL][F::PIECES], uint32_t (&sr)[F::UNROLL]) {
         const int b = min(iss_it * a.nb + my_nb, W.nblocks - 1);
-        load_batch<WB, GSZ, SF32>(W.data + (size_t)b * W.nchunks * W.rec, W.rec, W.nchunks,
-                                  my_kw + iss_bi * F::UNROLL * a.kw, a.kw, lane, w, sr);
+        load_batch<WB, GSZ, SF32>(wrs, (uint32_t)b * rb_bytes, rec, W.nchunks, my_kw + iss_bi * F::UNROLL * a.kw, a.kw,
+                                  lane, w, sr);
         if constexpr (EPI == EPI_RESID)
             if (iss_bi == 0 && iss_it != it0) pre_x_next = a.out[min(iss_it * rows_it + tid, W.rows - 1)];
         if (++iss_bi == bpi) {
@@ -380,9 +393,9 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
         if (lane < rb) sred[wave * rb + lane] = acc;
         __syncthreads();
         if (tid < rows_it) {
-            const int nbi = tid / rb, r = tid - nbi * rb;
+            const int nbi = tid >> a.rb_log2, r = tid & (rb - 1);
             float v = 0.0f;
-            for (int k = 0; k < a.kw; k++) v += sred[(nbi * a.kw + k) * rb + r];
+            for (int k = 0; k < a.kw; k++) v += sred[(k * a.nb + nbi) * rb + r];
             srow[tid] = v;
         }
         __syncthreads();
@@ -452,7 +465,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             // each row-block holds rb/2 gate rows then the rb/2 matching up rows (qwen.c:556-562)
             const int hb = rb / 2, per_it = a.nb * hb;
             if (tid < rows_it) {
-                const int nbi = tid / rb, r = tid - nbi * rb;
+                const int nbi = tid >> a.rb_log2, r = tid & (rb - 1);
                 if (r < hb) {
                     float g = srow[tid], u = srow[tid + hb];
                     float sig = 1.0f / (1.0f + expf(-g));
@@ -534,6 +547,12 @@ static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
     return hipGetLastError();
 }
 
+static int log2_exact(int v) { // log2 of a power of two, -1 otherwise
+    int k = 0;
+    while ((1 << k) < v) k++;
+    return (1 << k) == v ? k : -1;
+}
+
 template <int WB, int GSZ, int SF32>
 static hipError_t launch_fmt(int pro, int epi, const GemvArgs &a, int grid, hipStream_t st) {
 #define CASE(P, E) if (pro == P && epi == E) return launch_one<WB, GSZ, SF32, P, E>(a, grid, st)
@@ -547,10 +566,21 @@ static hipError_t launch_fmt(int pro, int epi, const GemvArgs &a, int grid, hipS
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &a, int grid, hipStream_t st) {
+hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &args, int grid, hipStream_t st) {
+    // quotients of the launch shape, so the kernel divides nothing: nb and rb are powers of two
+    GemvArgs a = args;
+    const int nb_log2 = log2_exact(a.nb), rb_log2 = log2_exact(a.W.rb);
+    if (nb_log2 < 0 || rb_log2 < 0 || a.kw < 1 || a.kw > a.W.nchunks || a.kw * a.nb > 16 || grid < 1) return hipErrorInvalidValue;
+    a.nb_log2 = nb_log2;
+    a.rb_log2 = rb_log2;
+    a.n_it = (a.W.nblocks + a.nb - 1) / a.nb;
+    a.kw_base = a.W.nchunks / a.kw;
+    a.kw_rem = a.W.nchunks % a.kw;
+    a.it_base = a.n_it / grid;
+    a.it_rem = a.n_it % grid;
     // the prologues read their inputs as 16-byte vectors (8 bytes for the attention statistics)
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
-    if (a.W.n % 32 || (pro == PRO_XQ && !al(a.xq, 16)) || (pro == PRO_NORM && (!al(a.x, 16) || !al(a.norm_w, 16))) ||
+    if (a.W.n % 32 || a.W.bytes >= 0x7fffffffu || (pro == PRO_XQ && !al(a.xq, 16)) || (pro == PRO_NORM && (!al(a.x, 16) || !al(a.norm_w, 16))) ||
         (pro == PRO_ATTN && (!al(a.att_acc, 16) || !al(a.att_ml, 8) || a.head_size % 4 || a.att_splits < 1 ||
                              a.att_splits > 64)))
         return hipErrorInvalidValue;
