@@ -7,6 +7,10 @@ greedy, batch 1.  A step is one decode position: the whole forward() plus the ar
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
   python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c3|c4|c5] [--no-cpu]
+  roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes:
+    rocprofv3 --pmc FETCH_SIZE -d D/fetch -- python bench.py --counters --profile-steps 4
+    rocprofv3 --pmc WRITE_SIZE -d D/write -- python bench.py --counters --profile-steps 4
+    python bench.py --traffic-from D ...
   (c4: the 512-token prompt as one batched int8-MFMA prefill, timed over --steps repetitions)
 
 Also reported: per-kernel roofline (HIP events around every launch on the library's stream, algorithmic
@@ -123,6 +127,57 @@ def greedy_parity(path, prompt, n_new, ctx, ids_gpu, logits_gpu):
     return out
 
 
+# HIP kernel of each step kernel kind (.qwb models: int4 layers, int8 head), as rocprofv3 names them
+KERNEL_SYMBOL = {"qkv_gemv": "k_gemv<4, 32, 0, 1, 2>", "o_gemv": "k_gemv<4, 32, 0, 2, 1>",
+                 "gateup_gemv": "k_gemv<4, 32, 0, 1, 3>", "down_gemv": "k_gemv<4, 32, 0, 0, 1>",
+                 "head_gemv": "k_gemv<8, 32, 0, 1, 4>", "attention": "k_attention", "step_start": "k_step_start"}
+CALIB_BYTES = 1 << 30  # the plain device copy that calibrates the byte counters (larger than any load copy)
+
+
+def calib_copy():
+    """a plain elementwise pass over CALIB_BYTES (reads them once, writes them once) for the counter scale"""
+    import torch
+    a = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    torch.mul(a, 2.0, out=b)
+    torch.cuda.synchronize()
+    del a, b
+    torch.cuda.empty_cache()
+
+
+def pmc_per_dispatch(csv_path, counter):
+    """{kernel name: [KiB per dispatch]} from a rocprofv3 --pmc counter_collection.csv"""
+    import csv
+    out = {}
+    for r in csv.DictReader(open(csv_path)):
+        if r["Counter_Name"] == counter:
+            out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return out
+
+
+def traffic_from(pmc_dir, kind):
+    """HBM bytes per launch of `kind` from two rocprofv3 --pmc passes over `bench.py --calib` (FETCH_SIZE in
+    pmc_dir/fetch, WRITE_SIZE in pmc_dir/write), each scaled by what the counter reads for the calibration copy
+    (CALIB_BYTES read and CALIB_BYTES written)"""
+    import glob
+    res = {}
+    for sub, counter in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        files = glob.glob(os.path.join(pmc_dir, sub, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return None
+        per = pmc_per_dispatch(files[0], counter)
+        copy = [v for k, vs in per.items() if "copy" in k.lower() or "elementwise" in k.lower() for v in vs]
+        sym = KERNEL_SYMBOL.get(kind)
+        vals = [v for k, vs in per.items() if sym and sym in k for v in vs]
+        if not copy or not vals:
+            return None
+        factor = max(copy) * 1024.0 / CALIB_BYTES  # counter bytes per real byte
+        res[sub] = sum(vals) / len(vals) * 1024.0 / factor
+        res[sub + "_factor"] = factor
+    return res
+
+
 def layer_macs(info):
     """multiply-accumulates of the layer matrices for one token (qkv, o, gate/up, down)"""
     kv = info.dim // info.n_heads * info.n_kv_heads
@@ -172,6 +227,11 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--cpu-tokens", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib", action="store_true", help="run the counter calibration copy first")
+    ap.add_argument("--counters", action="store_true",
+                    help="counter pass: the calibration copy, then the prompt and --profile-steps decode steps as "
+                         "eager launches only (no graphs), no report")
+    ap.add_argument("--traffic-from", default=None, help="directory with the FETCH_SIZE/WRITE_SIZE passes")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
@@ -186,6 +246,17 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.init()
+    if a.calib or a.counters:
+        calib_copy()
+    if a.counters:
+        P = load_pkg()
+        m = P.Model(path, cfg["ctx"])
+        for pos, t in enumerate(prompt):
+            m.forward(t, pos)
+        m.profile(a.profile_steps)
+        m.close()
+        log(f"counter pass: {len(prompt)} eager positions + {a.profile_steps} profiled steps")
+        return
     if a.config == "c4":
         return prefill_bench(a, cfg, path, prompt)
     P = load_pkg()
@@ -231,6 +302,10 @@ def main():
     gemv_s = sum(s["total_ms"] for s in gemv) * 1e-3
     m.close()
 
+    traffic = traffic_from(a.traffic_from, dom["name"]) if a.traffic_from else None
+    if traffic:
+        log(f"traffic of {dom['name']}: {traffic['fetch'] / 1e6:.3f} MB fetched + {traffic['write'] / 1e6:.3f} MB written "
+            f"per launch (counter factors {traffic['fetch_factor']:.3f} / {traffic['write_factor']:.3f})")
     cpu = None if a.no_cpu else cpu_baseline(path, prompt, a.cpu_tokens, cfg["ctx"])
     match = None if a.no_cpu else greedy_parity(path, prompt, a.cpu_tokens, cfg["ctx"], ids_gpu, gen["logits"])
 
@@ -243,7 +318,8 @@ def main():
         "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
                    "ctx": cfg["ctx"], "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
+                     "traffic": round(traffic["fetch"] + traffic["write"]) if traffic else None,
                      "avg_launch_us": round(dom_avg_s * 1e6, 3), "bytes_per_launch": round(dom["bytes_per_launch"])},
         "gemv_all": {"achieved": round(gemv_bytes / gemv_s / 1e9, 1), "unit": "GB/s",
                      "frac": round(gemv_bytes / gemv_s / 1e9 / PEAK_HBM, 4),
