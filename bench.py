@@ -6,7 +6,7 @@ with seeded head_ids; seeded N(0, 0.02) random-init weights written by host/synt
 greedy, batch 1.  A step is one decode position: the whole forward() plus the argmax on the device, one
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
-  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c3|c4|c5] [--no-cpu]
+  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu]
   roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes:
     rocprofv3 --pmc FETCH_SIZE -d D/fetch -- python bench.py --counters --profile-steps 4
     rocprofv3 --pmc WRITE_SIZE -d D/write -- python bench.py --counters --profile-steps 4
@@ -30,14 +30,24 @@ import numpy as np
 REPO = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(REPO, "local-llama-pynq-z2_amd")
 PEAK_HBM = 8000.0  # GB/s, MI355X
+METRIC = "decode tok/s + GEMV HBM GB/s (% of peak), Q4_0 Qwen2-0.5B shape, batch 1"
 CONFIGS = {
-    "c3": dict(preset="c3", seed=3, prompt=24, new=128, ctx=1024,
+    "c1": dict(fmt="bin", preset="c1", seed=1, prompt=8, new=240, ctx=0, ref="runq",
+               metric="decode tok/s + GEMV HBM GB/s (% of peak), Q8_0 llama2.c 288/6L shape, batch 1",
+               workload="llama2.c-style .bin decode (dim 288, 6 layers, 6 heads, FFN 768, vocab 32000, seq_len 256, "
+                        "Q8_0 group 32 with fp32 scales): 8-token prompt, greedy, batch 1"),
+    "c2": dict(fmt="bin", preset="c2", seed=2, prompt=8, new=512, ctx=0, ref="runq",
+               metric="decode tok/s + GEMV HBM GB/s (% of peak), Q8_0 llama2.c 768/12L shape, batch 1",
+               workload="llama2.c-style .bin decode (dim 768, 12 layers, 12 heads, FFN 2048, vocab 32000, seq_len "
+                        "1024, Q8_0 group 32 with fp32 scales): 8-token prompt, greedy, batch 1"),
+    "c3": dict(fmt="qwb", preset="c3", seed=3, prompt=24, new=128, ctx=1024, ref="qwen", metric=METRIC,
                workload="Qwen2-0.5B shape .qwb decode (dim 896, 24 layers, 14/2 heads, FFN 4864, Q4_0 layers, "
                         "Q8_0 65536-row head): 24-token prompt, 128 greedy tokens, batch 1"),
-    "c4": dict(preset="c3", seed=3, prompt=512, new=64, ctx=1024,
+    "c4": dict(fmt="qwb", preset="c3", seed=3, prompt=512, new=64, ctx=1024, ref="qwen", metric=METRIC,
                workload="Qwen2-0.5B shape .qwb prefill (dim 896, 24 layers, 14/2 heads, FFN 4864, Q4_0 layers): "
                         "512-token prompt as int8 MFMA GEMMs + causal attention, then 64 greedy tokens, batch 1"),
-    "c5": dict(preset="c5", seed=5, prompt=32, new=256, ctx=4096,
+    "c5": dict(fmt="qwb", preset="c5", seed=5, prompt=32, new=256, ctx=4096, ref="qwen",
+               metric="decode tok/s + GEMV HBM GB/s (% of peak), Q4_0 Qwen2-7B shape, batch 1",
                workload="Qwen2-7B shape .qwb decode (dim 3584, 28 layers, 28/4 heads of 128, FFN 18944, Q4_0 "
                         "layers, Q8_0 152064-row head): 32-token prompt, 256 greedy tokens, KV cache 4096, batch 1"),
 }
@@ -57,10 +67,10 @@ def log(msg):
 def model_file(cfg):
     d = os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench")
     os.makedirs(d, exist_ok=True)
-    path = os.path.join(d, f"{cfg['preset']}_s{cfg['seed']}.qwb")
+    path = os.path.join(d, f"{cfg['preset']}_s{cfg['seed']}.{cfg['fmt']}")
     if not os.path.exists(path):
         t = time.time()
-        subprocess.run([os.path.join(PKG, "host", "synth"), "qwb", path + ".tmp", cfg["preset"], str(cfg["seed"])],
+        subprocess.run([os.path.join(PKG, "host", "synth"), cfg["fmt"], path + ".tmp", cfg["preset"], str(cfg["seed"])],
                        check=True, capture_output=True)
         os.replace(path + ".tmp", path)
         log(f"wrote {path} ({os.path.getsize(path) / 2**20:.0f} MiB) in {time.time() - t:.1f} s")
@@ -77,37 +87,45 @@ def head_ids_of(path):
     return np.fromfile(path, np.int32, int(head_k), offset=off)
 
 
-def cpu_baseline(path, prompt, n_new, ctx):
-    """the reference's qwen.c (OpenMP build) on this host: bounded sample of the same workload"""
-    exe = os.path.join(REPO, "oracle", "_ref", "qwen_fast")
+def ref_args(cfg, path, prompt, n_new):
+    """command-line of the reference host for the workload: qwen.c counts -n in new tokens, runq.c in
+    positions (prompt included, runq.c:1200)"""
+    ids = ",".join(map(str, prompt))
+    if cfg["ref"] == "qwen":
+        return [path, "--ids", ids, "-t", "0", "-n", str(n_new), "-c", str(cfg["ctx"])]
+    return [path, "--ids", ids, "-t", "0", "-n", str(len(prompt) - 1 + n_new)]
+
+
+def cpu_baseline(cfg, path, prompt, n_new):
+    """the reference's qwen.c / runq.c (OpenMP build) on this host: bounded sample of the same workload"""
+    exe = os.path.join(REPO, "oracle", "_ref", "qwen_fast" if cfg["ref"] == "qwen" else "runq_ids_fast")
     if not os.path.exists(exe):
         return None
     threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
     t = time.time()
-    r = subprocess.run([exe, path, "--ids", ",".join(map(str, prompt)), "-t", "0", "-n", str(n_new), "-c", str(ctx)],
-                       capture_output=True, text=True, env=env, timeout=600)
+    r = subprocess.run([exe] + ref_args(cfg, path, prompt, n_new), capture_output=True, text=True, env=env, timeout=600)
     wall = time.time() - t
     m = re.search(r"generated: (\d+) tokens, ([0-9.]+) tok/s", r.stderr)
     if r.returncode != 0 or not m:
         log(f"cpu baseline failed: {r.stderr[-400:]}")
         return None
+    src = "qwen.c" if cfg["ref"] == "qwen" else "runq.c"
     return {"value": float(m.group(2)), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"qwen.c (OpenMP, -O3 -ffast-math -march=x86-64-v3) on the same .qwb: {len(prompt)}-token "
-                      f"prompt + {int(m.group(1))} greedy tokens, decode rate as qwen.c prints it ({wall:.1f} s wall)"}
+            "sample": f"{src} (OpenMP, -O3 -ffast-math -march=x86-64-v3) on the same .{cfg['fmt']}: {len(prompt)}-token "
+                      f"prompt + {int(m.group(1))} greedy tokens, decode rate in qwen.c's definition ({wall:.1f} s wall)"}
 
 
-def greedy_parity(path, prompt, n_new, ctx, ids_gpu, logits_gpu):
-    """the reference's qwen.c built strict IEEE (oracle/_ref/qwen): its greedy ids and --logits dump against
-    the device run; a divergence is reported with the reference's top-2 logit gap at that position"""
-    exe = os.path.join(REPO, "oracle", "_ref", "qwen")
+def greedy_parity(cfg, path, prompt, n_new, ids_gpu, logits_gpu):
+    """the reference's qwen.c / runq.c built strict IEEE (oracle/_ref/qwen, runq_ids): its greedy ids and
+    --logits dump against the device run; a divergence is reported with the reference's top-2 logit gap"""
+    exe = os.path.join(REPO, "oracle", "_ref", "qwen" if cfg["ref"] == "qwen" else "runq_ids")
     if not os.path.exists(exe):
         return None
     dump = os.path.join(os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench"), "ref.logits")
     threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
-    r = subprocess.run([exe, path, "--ids", ",".join(map(str, prompt)), "-t", "0", "-n", str(n_new), "-c", str(ctx),
-                        "--logits", dump], capture_output=True, text=True, timeout=900,
-                       env=dict(os.environ, OMP_NUM_THREADS=str(threads)))
+    r = subprocess.run([exe] + ref_args(cfg, path, prompt, n_new) + ["--logits", dump], capture_output=True, text=True,
+                       timeout=900, env=dict(os.environ, OMP_NUM_THREADS=str(threads)))
     if r.returncode != 0:
         return None
     ids_ref = [int(v) for v in r.stdout.strip().split(",") if v]
@@ -117,7 +135,8 @@ def greedy_parity(path, prompt, n_new, ctx, ids_gpu, logits_gpu):
     rows = min(len(ref), len(logits_gpu))
     upto = rows if div is None else len(prompt) + div  # positions on the shared token path
     errs = [float(np.abs(logits_gpu[p] - ref[p]).max() / np.abs(ref[p]).max()) for p in range(upto)]
-    out = {"reference": "qwen.c strict IEEE build", "tokens_compared": n, "identical": div is None,
+    out = {"reference": ("qwen.c" if cfg["ref"] == "qwen" else "runq.c") + " strict IEEE build", "tokens_compared": n,
+           "identical": div is None,
            "first_divergence": div, "logit_rel_err_max": max(errs) if errs else None,
            "logit_rel_err_median": float(np.median(errs)) if errs else None}
     if div is not None:
@@ -240,8 +259,13 @@ def main():
     cfg = CONFIGS[a.config]
     steps = a.steps or cfg["new"]
     path = model_file(cfg)
-    hid = head_ids_of(path)
-    prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).choice(hid, cfg["prompt"], replace=False)]
+    if cfg["fmt"] == "qwb":
+        hid = head_ids_of(path)
+        prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).choice(hid, cfg["prompt"], replace=False)]
+    else:  # runq: seeded ids from [2, vocab) (1 is BOS, which stops the generation)
+        with open(path, "rb") as f:
+            vocab = int(abs(np.frombuffer(f.read(64), np.int32, 1, 8 + 5 * 4)[0]))
+        prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).integers(2, vocab, cfg["prompt"])]
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
@@ -264,6 +288,7 @@ def main():
     m = P.Model(path, cfg["ctx"])
     log(f"model resident in {time.time() - t:.1f} s: {m.info.weight_bytes / 2**20:.0f} MiB of tiled weights, "
         f"{m.info.gemv_bytes_per_token / 1e6:.2f} MB GEMV bytes per token")
+    ctx_used = m.info.ctx
     if len(prompt) + 1 + max(steps, a.warmup, a.profile_steps) >= m.info.ctx:
         raise SystemExit("steps do not fit the context")
 
@@ -306,17 +331,18 @@ def main():
     if traffic:
         log(f"traffic of {dom['name']}: {traffic['fetch'] / 1e6:.3f} MB fetched + {traffic['write'] / 1e6:.3f} MB written "
             f"per launch (counter factors {traffic['fetch_factor']:.3f} / {traffic['write_factor']:.3f})")
-    cpu = None if a.no_cpu else cpu_baseline(path, prompt, a.cpu_tokens, cfg["ctx"])
-    match = None if a.no_cpu else greedy_parity(path, prompt, a.cpu_tokens, cfg["ctx"], ids_gpu, gen["logits"])
+    cpu = None if a.no_cpu else cpu_baseline(cfg, path, prompt, a.cpu_tokens)
+    match = None if a.no_cpu else greedy_parity(cfg, path, prompt, a.cpu_tokens, ids_gpu, gen["logits"])
 
     out = {
-        "metric": "decode tok/s + GEMV HBM GB/s (% of peak), Q4_0 Qwen2-0.5B shape, batch 1",
+        "metric": cfg["metric"],
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
         "ms_per_step": round(wall / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8",
-        "data": "synthetic: seeded N(0,0.02) random-init weights (Q4_0 layers, Q8_0 head), seeded prompt ids",
+        "data": "synthetic: seeded N(0,0.02) random-init weights (" + ("Q4_0 layers, Q8_0 head" if cfg["fmt"] == "qwb"
+                 else "Q8_0 with fp32 scales") + "), seeded prompt ids",
         "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
-                   "ctx": cfg["ctx"], "batch": 1},
+                   "ctx": ctx_used, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
                      "traffic": round(traffic["fetch"] + traffic["write"]) if traffic else None,

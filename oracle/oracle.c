@@ -188,9 +188,18 @@ void or_matvec_runq(float *out, const int8_t *wq, const float *ws, const int8_t 
 /* element-wise blocks */
 
 /* qwen.c:337-344 (runq.c:394-407 is the same with eps 1e-5f) */
+static int norm_ways = 1;
+void or_set_norm_ways(int k) { norm_ways = k >= 1 && k <= 8 ? k : 1; }
+
 void or_rmsnorm(float *o, const float *x, const float *w, int n, float eps) {
     float ss = 0.0f;
-    for (int j = 0; j < n; j++) ss += x[j] * x[j];
+    if (norm_ways == 1) {
+        for (int j = 0; j < n; j++) ss += x[j] * x[j];
+    } else { /* tolerance experiments only: k interleaved partial sums, added in order */
+        float part[8] = {0};
+        for (int j = 0; j < n; j++) part[j % norm_ways] += x[j] * x[j];
+        for (int k = 0; k < norm_ways; k++) ss += part[k];
+    }
     ss /= (float)n;
     ss += eps;
     ss = 1.0f / sqrtf(ss);

@@ -32,3 +32,8 @@ float *refr_forward(void *t, int token, int pos) { return forward((Transformer *
 int refr_vocab(void *t) { return ((Transformer *)t)->config.vocab_size; }
 int refr_seq_len(void *t) { return ((Transformer *)t)->config.seq_len; }
 int refr_argmax(float *p, int n) { return sample_argmax(p, n); }
+/* key (which 0) or value (1) cache of the reference's RunState: [n_layers][seq_len][kv_dim] */
+float *refr_kv(void *t, int which) {
+    Transformer *x = (Transformer *)t;
+    return which ? x->state.value_cache : x->state.key_cache;
+}
