@@ -78,6 +78,7 @@ struct AttnArgs {
     const float *kc, *vc;   // layer bases [ctx][kv_dim]
     float *ml, *acc;        // partials, see GemvArgs
     int n_heads, n_kv, hs, kv_dim, splits; // splits: maximum number of position slices (grid)
+    int max_pos;            // positions the cache holds (the launcher picks the kernel for the longest slice)
     const StepCtrl *ctrl;
 };
 

@@ -16,6 +16,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "attn.h"
 
 // ------------------------------------------------------------------------------------------------------
@@ -628,11 +630,141 @@ __global__ void __launch_bounds__(256) k_attention(AttnArgs a) {
     KERNEL_MARK(7);
 }
 
+// Decode attention when every slice has at most 64 positions (ATT_SHORT_MAX).  One block per (kv head,
+// slice): its threads stage the group's queries, the slice's K rows (padded to hs + 4 floats) and V rows in
+// LDS with one round of coalesced buffer loads (rows past the slice fall outside the buffer range and read
+// nothing), then wave j takes query head kvh * kv_mul + j with no further barrier.  Scores: lane t holds
+// position t0 + t and forms q . k in the reference's element order; the slice's max and sum of exponentials by
+// DPP.  Values: lane l holds elements EPL * l ..: the sum over t of exp(s_t - max) * v[t][e] in position order,
+// the weight taken from lane t.  Leaves the same per-slice partials as k_attention.
+#define ATT_SHORT_MAX 64
+#define ATT_SHORT_LOADS 8   // K (and V) loads per thread: ceil(ATT_SHORT_MAX / rows per pass) <= 8
+static inline size_t attn_short_lds_floats(int kv_mul, int hs) {
+    return (size_t)kv_mul * hs + (size_t)ATT_SHORT_MAX * (hs + 4) + (size_t)ATT_SHORT_MAX * hs;
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(512) k_attention_short(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    const int pos = a.ctrl->pos;
+    const int kvh = blockIdx.x / a.splits, s = blockIdx.x - kvh * a.splits;
+    int S, chunk;
+    att_slices(pos, a.splits, &S, &chunk);
+    if (s >= S) return;
+    KERNEL_MARK(0);
+    const int kv_mul = a.n_heads / a.n_kv, hs = a.hs, hs4 = hs / 4, ks = hs + 4, nt = blockDim.x;
+    const int tid = threadIdx.x, t0 = s * chunk, T = min(chunk, pos + 1 - t0); // 1 <= T <= 64
+    float *sq = sm, *sk = sq + kv_mul * hs, *sv = sk + ATT_SHORT_MAX * ks;
+    {
+        const auto rq = __builtin_amdgcn_make_buffer_rsrc((void *)(a.q + (size_t)kvh * kv_mul * hs), 0,
+                                                          kv_mul * hs * 4, 0x00020000);
+        const size_t kv_off = (size_t)t0 * a.kv_dim + (size_t)kvh * hs;
+        const int span = ((T - 1) * a.kv_dim + hs) * 4;
+        const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(a.kc + kv_off), 0, span, 0x00020000);
+        const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + kv_off), 0, span, 0x00020000);
+        const int rs = nt / hs4, r0 = tid / hs4, c = tid - r0 * hs4; // rows per pass, this thread's row, column
+        const unsigned OUT = 0x40000000u;                             // past every range: reads nothing
+        const auto qv = __builtin_amdgcn_raw_buffer_load_b128(rq, tid < kv_mul * hs4 ? tid * 16 : OUT, 0, 0);
+        u32x4 kr[ATT_SHORT_LOADS], vr[ATT_SHORT_LOADS];
+#pragma unroll
+        for (int k = 0; k < ATT_SHORT_LOADS; k++) {
+            const int t = r0 + k * rs;
+            const unsigned o = (r0 < rs && t < T) ? (unsigned)(t * a.kv_dim + 4 * c) * 4 : OUT;
+            kr[k] = __builtin_amdgcn_raw_buffer_load_b128(rk, o, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < ATT_SHORT_LOADS; k++) {
+            const int t = r0 + k * rs;
+            const unsigned o = (r0 < rs && t < T) ? (unsigned)(t * a.kv_dim + 4 * c) * 4 : OUT;
+            vr[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, o, 0, 0);
+        }
+        if (tid < kv_mul * hs4) *(u32x4 *)(sq + 4 * tid) = qv;
+#pragma unroll
+        for (int k = 0; k < ATT_SHORT_LOADS; k++) {
+            const int t = r0 + k * rs;
+            if (r0 < rs && t < T) *(u32x4 *)(sk + t * ks + 4 * c) = kr[k];
+        }
+#pragma unroll
+        for (int k = 0; k < ATT_SHORT_LOADS; k++) {
+            const int t = r0 + k * rs;
+            if (r0 < rs && t < T) *(u32x4 *)(sv + t * hs + 4 * c) = vr[k];
+        }
+    }
+    __syncthreads();
+    KERNEL_MARK(1);
+    const int j = __builtin_amdgcn_readfirstlane(tid / WAVE), lane = tid & (WAVE - 1);
+    if (j >= kv_mul) return;
+    const int h = kvh * kv_mul + j;
+    const f32x4 *k4 = (const f32x4 *)(sk + min(lane, T - 1) * ks), *q4 = (const f32x4 *)(sq + j * hs);
+    float d = 0.0f;
+#pragma unroll 4
+    for (int c4 = 0; c4 < hs4; c4++) {
+        const f32x4 kk = k4[c4], qq = q4[c4];
+        d += qq.x * kk.x;
+        d += qq.y * kk.y;
+        d += qq.z * kk.z;
+        d += qq.w * kk.w;
+    }
+    const bool valid = lane < T;
+    const float score = d / sqrtf((float)hs);
+    const float mx = wave_max(valid ? score : -INFINITY);
+    const float w = valid ? expf(score - mx) : 0.0f;
+    const float l = wave_sum(w);
+    KERNEL_MARK(2);
+    const int e = min(lane * EPL, hs - EPL);
+    const float *vp = sv + e;
+    float acc[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) acc[i] = 0.0f;
+    int t = 0;
+    for (; t + 8 <= T; t += 8) {
+        float v[8][EPL];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int i = 0; i < EPL; i++) v[u][i] = vp[(t + u) * hs + i];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t + u));
+#pragma unroll
+            for (int i = 0; i < EPL; i++) acc[i] += p * v[u][i];
+        }
+    }
+    for (; t < T; t++) {
+        const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), t));
+#pragma unroll
+        for (int i = 0; i < EPL; i++) acc[i] += p * vp[t * hs + i];
+    }
+    if (lane * EPL < hs) {
+        float *o = a.acc + ((size_t)h * a.splits + s) * hs + lane * EPL;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) o[i] = acc[i];
+    }
+    if (lane == 0) {
+        float *ml = a.ml + ((size_t)h * a.splits + s) * 2;
+        ml[0] = mx;
+        ml[1] = l;
+    }
+    KERNEL_MARK(7);
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
-    const int kv_mul = a.n_heads / a.n_kv, threads = 256;
-    if (kv_mul * a.hs > 4 * threads || a.hs % 4 || a.hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) ||
-        ((uintptr_t)a.vc & 15) || (a.kv_dim % 4))
+    const int kv_mul = a.n_heads / a.n_kv;
+    if (a.hs % 4 || a.hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) ||
+        (a.kv_dim % 4) || a.splits < 1 || a.max_pos < 1)
         return hipErrorInvalidValue;
+    // longest slice over every position the cache holds: ceil(P / S) with S = min(splits, ceil(P / ATT_SUB))
+    const int longest = std::max(ATT_SUB, (a.max_pos + a.splits - 1) / a.splits);
+    const int nt = WAVE * std::max(kv_mul, 4);
+    if (longest <= ATT_SHORT_MAX && kv_mul <= 8 && (a.hs % 4) == 0 && a.hs <= 2 * WAVE &&
+        (ATT_SHORT_MAX + nt / (a.hs / 4) - 1) / (nt / (a.hs / 4)) <= ATT_SHORT_LOADS) {
+        const size_t lds = attn_short_lds_floats(kv_mul, a.hs) * 4;
+        if (a.hs <= WAVE) hipLaunchKernelGGL(k_attention_short<1>, dim3(a.n_kv * a.splits), dim3(nt), lds, st, a);
+        else hipLaunchKernelGGL(k_attention_short<2>, dim3(a.n_kv * a.splits), dim3(nt), lds, st, a);
+        return hipGetLastError();
+    }
+    const int threads = 256;
+    if (kv_mul * a.hs > 4 * threads) return hipErrorInvalidValue;
     const size_t lds = attn_lds_floats(kv_mul, a.hs) * 4;
     hipLaunchKernelGGL(k_attention, dim3(a.n_kv * a.splits), dim3(threads), lds, st, a);
     return hipGetLastError();

@@ -220,6 +220,7 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         t.hs = m->hs;
         t.kv_dim = kv;
         t.splits = m->att_splits;
+        t.max_pos = m->ctx;
         t.ctrl = m->ctrl;
         mark(K_ATTN, attn_bytes(m, pos_hint));
         HIP_OR_FAIL("llm", launch_attention(t, m->st));

@@ -123,6 +123,31 @@ def test_runq_c1_shape(tmp_path):
     deep_bar(errs, div, gap, ids_o, ids_g)
 
 
+@pytest.mark.parametrize("shape", [("dim=128", "heads=4", "kv_heads=2"), ("dim=256", "heads=4", "kv_heads=1"),
+                                   ("dim=256", "heads=2", "kv_heads=1")])
+def test_decode_attention_at_long_context(tmp_path, shape):
+    """head sizes 32/64/128: positions 4000..4095 decoded after a 4000-token prefill.  A 4096-position cache
+    splits them into 64 slices of at most 64 positions (the one-wave-per-head register kernel); an
+    8192-position cache runs the same slices through the LDS-staged kernel.  Both hold bitwise the same
+    prefilled cache; both are held to the oracle's logits (flip-limited bar) and to each other."""
+    n0, n1 = 4000, 4096
+    p = synth("qwb", str(tmp_path / "long.qwb"), "tiny", 41, "layers=1", "max_seq=8192", *shape)
+    om = OracleModel(p, n1)
+    ids = [int(om.head_ids[v]) for v in np.random.default_rng(12).integers(0, om.n, n1)]
+    ref = [om.forward(t, pos) for pos, t in enumerate(ids)][n0:]
+    om.close()
+    got = []
+    for ctx in (4096, 8192):
+        m = pkg().Model(p, ctx)
+        m.prefill(ids[:n0])
+        got.append([m.forward(t, pos) for pos, t in enumerate(ids[n0:], n0)])
+        m.close()
+    for g in got:
+        errs = [rel_err(a, b) for a, b in zip(g, ref)]
+        assert np.median(errs) < 1e-4 and max(errs) < 2e-2, errs
+    assert np.median([rel_err(a, b) for a, b in zip(got[0], got[1])]) < 1e-5
+
+
 def test_decode_replay_and_profile_run():
     m = pkg().Model(os.path.join(GOLDEN, "tiny.qwb"), 64)
     m.generate(META["qwb"]["prompt"], 4)
