@@ -13,9 +13,10 @@ hipGraph replay.  `value` = timed steps / wall time between two device-wide sync
     python bench.py --traffic-from D ...
   (c4: the 512-token prompt as one batched int8-MFMA prefill, timed over --steps repetitions)
 
-Also reported: per-kernel roofline (HIP events around every launch on the library's stream, algorithmic
-bytes per launch), the greedy ids against the reference's own qwen.c, and that qwen.c (built with OpenMP,
--O3 -ffast-math, oracle/_ref/qwen_fast) timed on this host's cores on a bounded sample of the workload."""
+Also reported: per-kernel roofline (each kernel kind's device time inside the replayed step graph, from HIP
+events around graph replays with and without that kind's launches, and its algorithmic bytes per launch),
+the greedy ids against the reference's own qwen.c, and that qwen.c (built with OpenMP, -O3 -ffast-math,
+oracle/_ref/qwen_fast) timed on this host's cores on a bounded sample of the workload."""
 import argparse
 import importlib.util
 import json
@@ -311,14 +312,23 @@ def main():
     tok_s = steps / wall
     log(f"timed {steps} decode steps: {wall * 1e3:.2f} ms wall, {ev_ms:.2f} ms by events -> {tok_s:.1f} tok/s")
 
-    # per-kernel roofline (HIP events on the library's stream)
+    # per-kernel roofline: each kernel kind's time inside the replayed step graph (HIP events around graph
+    # replays with and without that kind's launches, on the library's stream); eager per-launch event times,
+    # which add launch and event overhead to every kernel, are logged beside them
     m.generate(prompt, 1)
-    stats = m.profile(a.profile_steps)
+    eager = {s["name"]: s for s in m.profile(a.profile_steps)}
+    m.generate(prompt, 1)
+    stats, step_ms = m.profile_graph(a.profile_steps, rounds=3)
     total = sum(s["total_ms"] for s in stats)
+    log(f"in-graph kernel times over {a.profile_steps} replayed steps (median step {step_ms * 1e3:.1f} us, "
+        f"sum of kinds {total / a.profile_steps * 1e3:.1f} us):")
     for s in sorted(stats, key=lambda s: -s["total_ms"]):
         avg = s["total_ms"] / s["launches"]
-        log(f"  {s['name']:12s} {s['launches']:6d} launches  avg {avg * 1e3:8.2f} us  {s['total_ms'] / total * 100:5.1f}%"
-            f"  {s['bytes_per_launch'] / 1e6:8.3f} MB  {s['bytes_per_launch'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
+        e = eager.get(s["name"])
+        e_us = f"{e['total_ms'] / e['launches'] * 1e3:8.2f}" if e else "     -  "
+        log(f"  {s['name']:12s} {s['launches']:6d} launches  avg {avg * 1e3:8.2f} us (eager {e_us} us)"
+            f"  {s['total_ms'] / total * 100:5.1f}%  {s['bytes_per_launch'] / 1e6:8.3f} MB"
+            f"  {s['bytes_per_launch'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
     dom = max(stats, key=lambda s: s["total_ms"])
     dom_avg_s = dom["total_ms"] / dom["launches"] * 1e-3
     achieved = dom["bytes_per_launch"] / dom_avg_s / 1e9

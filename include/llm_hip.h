@@ -75,6 +75,14 @@ typedef struct {
 } llm_kernel_stat;
 int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int max_stats);
 
+/* Per-kernel time inside the replayed step graph: the graph is replayed `steps` times from the current
+ * position, and again with each kernel kind's launches left out (`rounds` alternating repetitions, medians);
+ * a kind's total_ms is the difference, i.e. its device time in the graph including its share of the gaps
+ * between nodes, with no launch or event overhead.  *step_ms receives the median full-step time.  The step
+ * control (position, next token) is restored afterwards; the KV rows the replays wrote lie past it and are
+ * rewritten by the next steps.  Returns the number of records, or -1. */
+int llm_profile_graph(llm_model *m, int steps, int rounds, llm_kernel_stat *stats, int max_stats, double *step_ms);
+
 /* Batched prompt processing (prefill; the reference runs the prompt one forward() per position,
  * qwen.c:674-681): positions 0..n-1 pass through each layer together, in chunks of up to 512 tokens.  The
  * layer matrices become int8 MFMA GEMMs with exact int32 group sums and the reference's per-group product
@@ -86,6 +94,15 @@ int llm_prefill(llm_model *m, const int *ids, int n, float *logits);
  * position.  The --logits history (llm_generate with `logits`) always uses the per-position steps. */
 int llm_set_prefill(llm_model *m, int on);
 
+/* Sampling in llm_generate (the reference's sampler, qwen.c:578-654 / runq.c:830-967, which its hosts run on
+ * the CPU per token): with temperature > 0 every generated token is drawn on the device inside the step
+ * graph (logits / temperature, softmax, top-p when 0 < topp < 1 else the plain cdf walk, xorshift64* coin
+ * from `seed`); temperature 0 restores greedy argmax.  The RNG state lives on the device and advances once
+ * per drawn token, as the reference's does; forced prompt positions draw nothing.  Returns 0 or -1. */
+int llm_set_sampler(llm_model *m, float temperature, float topp, unsigned long long seed);
+/* the sampler's current RNG state (0 before llm_set_sampler) */
+int llm_sampler_state(llm_model *m, unsigned long long *rng);
+
 void llm_close(llm_model *m);
 
 /* ---- test hooks: no counterpart in the reference; they expose single device stages so the tests can
@@ -96,6 +113,10 @@ int mvh_quantize(const float *x, int n, int flavor, int gs, int8_t *q, float *s)
 /* exact int32 group sums of a matrix in the reference layout (qwen planes: bits 4 or 8, group 32; or runq
  * int8 with group gs when bits == 0), computed by the GEMV kernels' own dot-product code: ival[d][n/gs] */
 int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, int bits, int gs, int32_t *ival);
+/* the on-device sampler on caller logits: `count` vectors of n logits drawn one after another with one RNG
+ * state (*rng in, the advanced state out), temperature > 0; rows[count] receives the sampled rows */
+int mvh_sample(const float *logits, int n, int count, float temperature, float topp, unsigned long long *rng,
+               int *rows);
 /* the prefill GEMM on caller data: y[m][r] for M tokens, weights in the reference layout (qwen planes: bits 4
  * or 8 with fp16 scales, group 32; runq: bits 0 = int8 with fp32 scales, group gs), tiled with row-blocks of
  * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d] */

@@ -71,6 +71,7 @@ def lib():
     L.llm_generate.argtypes = [vp, vp, i32, i32, vp, vp, C.POINTER(LlmTiming)]
     L.llm_decode_replay.argtypes = [vp, i32, C.POINTER(C.c_double)]
     L.llm_profile.argtypes = [vp, i32, C.POINTER(LlmKernelStat), i32]
+    L.llm_profile_graph.argtypes = [vp, i32, i32, C.POINTER(LlmKernelStat), i32, C.POINTER(C.c_double)]
     L.llm_prefill.argtypes = [vp, vp, i32, vp]
     L.llm_close.argtypes = [vp]
     L.llm_close.restype = None
@@ -79,6 +80,9 @@ def lib():
     L.mvh_group_dots.argtypes = [vp, vp, i32, i32, i32, i32, vp]
     L.mvh_prefill_gemm.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
     L.llm_set_prefill.argtypes = [vp, i32]
+    L.llm_set_sampler.argtypes = [vp, C.c_float, C.c_float, C.c_ulonglong]
+    L.llm_sampler_state.argtypes = [vp, C.POINTER(C.c_ulonglong)]
+    L.mvh_sample.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
     _lib = L
     return L
 
@@ -120,6 +124,17 @@ def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16):
     if lib().mvh_prefill_gemm(_ptr(w), _ptr(ws), _ptr(xq), _ptr(xs), M, n, d, bits, gs, rb, _ptr(y)) != 0:
         raise RuntimeError("mvh_prefill_gemm failed")
     return y
+
+
+def sample(logits, temperature, topp, seed):
+    """The on-device sampler on caller logits [count, n] (or [n]), drawn in order with one RNG state seeded by
+    `seed`: (rows, the advanced RNG state)."""
+    lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
+    rows = np.empty(lg.shape[0], np.int32)
+    st = C.c_ulonglong(seed)
+    if lib().mvh_sample(_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)) != 0:
+        raise RuntimeError("mvh_sample failed")
+    return rows, st.value
 
 
 # ---- drop-in driver API -----------------------------------------------------------------------------------
@@ -212,6 +227,17 @@ class Model:
         return [{"name": st[i].name.decode(), "launches": st[i].launches, "total_ms": st[i].total_ms,
                  "bytes_per_launch": st[i].bytes_per_launch} for i in range(n)]
 
+    def profile_graph(self, steps, rounds=3):
+        """per-kernel-kind device time inside the replayed step graph (see llm_profile_graph); returns
+        (records, median step ms)"""
+        st = (LlmKernelStat * 16)()
+        step = C.c_double(0.0)
+        n = self.L.llm_profile_graph(self.h, steps, rounds, st, 16, C.byref(step))
+        if n < 0:
+            raise RuntimeError("llm_profile_graph failed")
+        return [{"name": st[i].name.decode(), "launches": st[i].launches, "total_ms": st[i].total_ms,
+                 "bytes_per_launch": st[i].bytes_per_launch} for i in range(n)], step.value
+
     def read_state(self, which, layer=0, count=None):
         n = self.info.dim if which == 0 else self.info.ctx * (self.info.dim // self.info.n_heads * self.info.n_kv_heads)
         if count is not None:
@@ -220,6 +246,18 @@ class Model:
         if self.L.llm_read_state(self.h, which, layer, _ptr(out), n) != 0:
             raise RuntimeError("llm_read_state failed")
         return out
+
+    def set_sampler(self, temperature, topp=0.9, seed=1):
+        """temperature > 0: generate() draws tokens on the device (temperature, top-p, xorshift coin from
+        seed); 0: greedy"""
+        if self.L.llm_set_sampler(self.h, temperature, topp, seed) != 0:
+            raise RuntimeError("llm_set_sampler failed")
+
+    def sampler_state(self):
+        st = C.c_ulonglong(0)
+        if self.L.llm_sampler_state(self.h, C.byref(st)) != 0:
+            raise RuntimeError("llm_sampler_state failed")
+        return st.value
 
     def set_prefill(self, on):
         """whether generate() runs the prompt as one batched prefill (default) or one step per position"""

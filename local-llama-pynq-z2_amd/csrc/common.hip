@@ -50,6 +50,7 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
         s.grid = iters;
     }
     if (s.grid < 1) s.grid = 1;
+    s.depth = 2;
     return s;
 }
 

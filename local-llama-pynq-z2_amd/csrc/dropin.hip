@@ -129,6 +129,7 @@ int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out
     a.W = W->T;
     a.kw = W->shape.kw;
     a.nb = W->shape.nb;
+    a.depth = W->shape.depth;
     a.xq = xdev;
     a.xs = (const float *)xs;
     a.out = (float *)out;

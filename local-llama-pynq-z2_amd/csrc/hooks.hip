@@ -145,3 +145,55 @@ extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *
     hipFree(dmap);
     return rc;
 }
+
+extern "C" int mvh_sample(const float *logits, int n, int count, float temperature, float topp,
+                          unsigned long long *rng, int *rows) {
+    if (!logits || !rng || !rows || n < 2 || count < 1 || !(temperature > 0.0f)) {
+        fprintf(stderr, "mvh_sample: bad arguments (n=%d count=%d temperature=%g)\n", n, count, temperature);
+        return -1;
+    }
+    if (hook_device("mvh_sample")) return -1;
+    float *dl = nullptr, *dp = nullptr;
+    unsigned *dk = nullptr;
+    int *di = nullptr, *dr = nullptr;
+    SamplerState *dss = nullptr;
+    SamplerState st;
+    st.temperature = temperature;
+    st.topp = topp;
+    st.rng = *rng;
+    int rc = -1;
+    if (hipMalloc(&dl, (size_t)count * n * 4) == hipSuccess && hipMalloc(&dp, (size_t)n * 4) == hipSuccess &&
+        hipMalloc(&dk, (size_t)2 * n * 4) == hipSuccess && hipMalloc(&di, (size_t)2 * n * 4) == hipSuccess &&
+        hipMalloc(&dr, (size_t)count * 4) == hipSuccess && hipMalloc(&dss, sizeof st) == hipSuccess &&
+        hipMemcpy(dl, logits, (size_t)count * n * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dss, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess) {
+        rc = 0;
+        for (int c = 0; c < count && !rc; c++) {
+            SampleArgs a;
+            memset(&a, 0, sizeof a);
+            a.logits = dl + (size_t)c * n;
+            a.n = n;
+            a.probs = dp;
+            a.key[0] = dk;
+            a.key[1] = dk + n;
+            a.idx[0] = di;
+            a.idx[1] = di + n;
+            a.ss = dss;
+            a.out_row = dr + c;
+            if (launch_sample(a, 0) != hipSuccess) rc = -1;
+        }
+        if (!rc && (hipDeviceSynchronize() != hipSuccess ||
+                    hipMemcpy(rows, dr, (size_t)count * 4, hipMemcpyDeviceToHost) != hipSuccess ||
+                    hipMemcpy(&st, dss, sizeof st, hipMemcpyDeviceToHost) != hipSuccess))
+            rc = -1;
+    }
+    if (rc) fprintf(stderr, "mvh_sample: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    else *rng = st.rng;
+    hipFree(dl);
+    hipFree(dp);
+    hipFree(dk);
+    hipFree(di);
+    hipFree(dr);
+    hipFree(dss);
+    return rc;
+}

@@ -34,7 +34,7 @@ static inline int hip_device_from_env(const char *who) {
 // block iteration, and the grid.  `ordered` keeps each row's groups in one lane, summed in order.  `cus` is
 // the device's compute-unit count (hip_cu_count).
 struct GemvShape {
-    int kw, nb, grid;
+    int kw, nb, grid, depth;
 };
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus);
 

@@ -40,6 +40,7 @@ enum { ROPE_NEOX = 0, ROPE_INTERLEAVED = 1 };
 struct GemvArgs {
     TiledMat W;
     int kw, nb;             // waves per row-block, row-blocks per block iteration (a power of two)
+    int depth;              // weight batches in flight per wave: 2 or 4
     // derived by launch_gemv: log2(nb), log2(W.rb), iterations, chunks per wave (kw_base + (my_kw < kw_rem)),
     // iterations per block (it_base + (block < it_rem))
     int nb_log2, rb_log2, n_it, kw_base, kw_rem, it_base, it_rem;
@@ -106,6 +107,27 @@ struct ArgmaxArgs {
     StepCtrl *ctrl;
     int *gen;               // [ctx] argmax result of every position
 };
+
+// Device-resident sampler settings and RNG state (the reference's Sampler, qwen.c:583-589).
+struct SamplerState {
+    float temperature, topp;
+    unsigned long long rng;
+};
+
+struct SampleArgs {
+    const float *logits;    // [n] head logits
+    int n;
+    float *probs;           // [n] scratch: probabilities
+    unsigned *key[2];       // [n] each: candidate sort keys (ping-pong)
+    int *idx[2];            // [n] each: candidate rows
+    SamplerState *ss;
+    const StepCtrl *ctrl;   // generate mode: no draw while the next token is a prompt token; NULL: always draw
+    float *pv;              // [np] argmax partials of the step: the choice becomes the only finite entry
+    int *pi;
+    int np;
+    int *out_row;           // optional: the sampled row
+};
+hipError_t launch_sample(const SampleArgs &a, hipStream_t st);
 
 struct RepackArgs {
     TiledMat T;             // output (T.data writable)

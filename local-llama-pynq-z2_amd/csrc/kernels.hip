@@ -171,8 +171,8 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // Slices of attention partials one merge pass loads per thread.
 #define MERGE_KB 8
 
-template <int WB, int GSZ, int SF32, int PRO, int EPI>
-__global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
+template <int WB, int GSZ, int SF32, int PRO, int EPI, int D>
+__global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     using F = Fmt<WB, GSZ, SF32>;
     extern __shared__ __align__(16) uint8_t lds[];
     const TiledMat &W = a.W;
@@ -188,7 +188,6 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
     // wave = my_kw * nb + my_nb (nb a power of two); the launcher precomputes every quotient the shape needs
     const int my_nb = wave & (a.nb - 1), my_kw = wave >> a.nb_log2;
     const int rows_it = a.nb * rb;
-    const int n_it = a.n_it;
     const int g_lane = lane >> a.rb_log2;
     const int it0 = blockIdx.x;
     KERNEL_MARK(0);
@@ -235,9 +234,9 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
 
     asm volatile("" ::: "memory"); // keep the issue order: prologue operands, then weights
 
-    // (2) the wave's first two weight batches.  The batches of all the block's iterations (it0, it0 + grid,
-    // ...) form one stream per wave: bpi batches per iteration, two buffers, and the next iteration's first
-    // batch is in flight while the current one is reduced and finished.
+    // (2) the wave's first D weight batches.  The batches of all the block's iterations (it0, it0 + grid,
+    // ...) form one stream per wave: bpi batches per iteration, D register buffers in a ring, and the next
+    // iteration's first batches are in flight while the current one is reduced and finished.
     const int cnt_w = a.kw_base + (my_kw < a.kw_rem);           // chunks of a row-block for this wave (>= 1)
     const int bpi = (cnt_w + F::UNROLL - 1) / F::UNROLL;         // batches per iteration
     const int n_my = a.it_base + (it0 < a.it_rem);               // iterations it0, it0 + grid, ... < n_it
@@ -257,10 +256,11 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             iss_it += gridDim.x;
         }
     };
-    uint4 wa[F::UNROLL][F::PIECES], wb[F::UNROLL][F::PIECES];
-    uint32_t sa[F::UNROLL], sb[F::UNROLL];
-    if (total > 0) issue(wa, sa);
-    if (total > 1) issue(wb, sb);
+    uint4 wr[D][F::UNROLL][F::PIECES];
+    uint32_t sr[D][F::UNROLL];
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (total > d) issue(wr[d], sr[d]);
 
     // (3) the epilogue operands of this thread's first row (clamped row index, used only for valid rows)
     float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f;
@@ -487,7 +487,7 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
         __syncthreads();
     };
 
-    // (6) the stream: consume a batch, refill its buffer with the batch two ahead
+    // (6) the stream: consume a batch, refill its buffer with the batch D ahead
     int use_it = it0, use_bi = 0;
     float acc = 0.0f;
     auto consume = [&](const uint4 (&w)[F::UNROLL][F::PIECES], const uint32_t (&sr)[F::UNROLL]) {
@@ -501,12 +501,13 @@ __global__ void __launch_bounds__(1024) k_gemv(GemvArgs a) {
             use_it += gridDim.x;
         }
     };
-    for (int q = 0; q < total; q += 2) {
-        consume(wa, sa);
-        if (q + 2 < total) issue(wa, sa);
-        if (q + 1 >= total) break;
-        consume(wb, sb);
-        if (q + 3 < total) issue(wb, sb);
+    for (int q = 0; q < total; q += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (q + d < total) {
+                consume(wr[d], sr[d]);
+                if (q + d + D < total) issue(wr[d], sr[d]);
+            }
     }
     if constexpr (EPI == EPI_ARGMAX) {
         // block argmax: larger value wins, equal values keep the lower row (first strict maximum)
@@ -545,7 +546,8 @@ template <int WB, int GSZ, int SF32, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
     const int threads = a.kw * a.nb * WAVE;
     const size_t lds = gemv_lds_bytes(a, PRO, EPI, threads);
-    hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI>), dim3(grid), dim3(threads), lds, st, a);
+    if (a.depth == 4) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4>), dim3(grid), dim3(threads), lds, st, a);
+    else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2>), dim3(grid), dim3(threads), lds, st, a);
     return hipGetLastError();
 }
 
@@ -580,6 +582,11 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
     a.kw_rem = a.W.nchunks % a.kw;
     a.it_base = a.n_it / grid;
     a.it_rem = a.n_it % grid;
+    // stream depth: 2 or 4 batches in flight per wave.  The residual epilogue preloads the next iteration's
+    // output rows one iteration ahead, which needs at least depth - 1 batches per iteration.
+    const int pieces = gs * wbits / 8 / 16, unroll = pieces > 0 && pieces <= 4 ? 4 / pieces : 1; // Fmt::UNROLL
+    // Depth 4 holds twice the registers: blocks of at most 8 waves.
+    if (a.depth != 4 || a.kw * a.nb > 8 || (epi == EPI_RESID && (a.kw_base + unroll - 1) / unroll < 3)) a.depth = 2;
     // the prologues read their inputs as 16-byte vectors (8 bytes for the attention statistics)
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
     if (a.W.n % 32 || a.W.bytes >= 0x7fffffffu || (pro == PRO_XQ && !al(a.xq, 16)) || (pro == PRO_NORM && (!al(a.x, 16) || !al(a.norm_w, 16))) ||

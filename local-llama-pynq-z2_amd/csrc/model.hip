@@ -72,6 +72,13 @@ struct llm_model {
     StepCtrl *ctrl = nullptr;
     int *prompt = nullptr, *tokens = nullptr, *gen = nullptr;
     hipGraphExec_t g_plain = nullptr, g_hist = nullptr;
+    // on-device sampler (temperature > 0): settings and RNG on the device, scratch, the sampling step graphs
+    bool sampling = false;
+    SamplerState *ss = nullptr;
+    float *smp_p = nullptr;
+    unsigned *smp_key = nullptr;
+    int *smp_idx = nullptr;
+    hipGraphExec_t g_plain_s = nullptr, g_hist_s = nullptr;
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, prefill_on = 1;
     float *pf_x = nullptr, *pf_y = nullptr, *pf_q = nullptr, *pf_z = nullptr, *pf_s = nullptr;
@@ -106,6 +113,7 @@ GemvArgs base_args(const llm_model *m, const TiledMat &T, const GemvShape &s) {
     a.W = T;
     a.kw = s.kw;
     a.nb = s.nb;
+    a.depth = s.depth;
     a.qflavor = m->qflavor;
     a.ctrl = m->ctrl;
     a.eps = m->info.rms_eps;
@@ -131,6 +139,23 @@ hipError_t launch_finalize(llm_model *m) {
     return launch_argmax(g, m->st);
 }
 
+// algorithmic bytes of one launch of a kernel kind (attention at position pos)
+double kind_bytes(const llm_model *m, int kind, int pos) {
+    const llm_info &I = m->info;
+    const int dim = I.dim, wb = m->kind == 0 ? 4 : 8, sf = m->kind == 0 ? 0 : 1;
+    switch (kind) {
+    case K_EMBED: return dim + dim / m->gs * (m->emb_sf32 ? 4.0 : 2.0) + dim * 4.0;
+    case K_QKV: return gemv_algo_bytes(m->L[0].qkv.rows, dim, wb, m->gs, sf);
+    case K_ATTN: return attn_bytes(m, pos);
+    case K_O: return gemv_algo_bytes(dim, dim, wb, m->gs, sf);
+    case K_GU: return gemv_algo_bytes(m->L[0].gu.rows, dim, wb, m->gs, sf);
+    case K_DOWN: return gemv_algo_bytes(dim, I.hidden_dim, wb, m->gs, sf);
+    case K_HEAD: return gemv_algo_bytes(m->head.rows, dim, 8, m->gs, m->head.sf32);
+    case K_ARGMAX: return m->s_head.grid * 8.0;
+    }
+    return 0;
+}
+
 // final rmsnorm + head GEMV of m->x (qwen.c:568-572): logits and per-block argmax partials
 hipError_t launch_head(llm_model *m, bool hist) {
     GemvArgs a = base_args(m, m->head, m->s_head);
@@ -143,8 +168,30 @@ hipError_t launch_head(llm_model *m, bool hist) {
     return launch_gemv(8, m->gs, m->head.sf32, PRO_NORM, EPI_ARGMAX, a, m->s_head.grid, m->st);
 }
 
-// Enqueue one decode step on m->st.  prof != NULL records events around every launch.
-int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finalize) {
+// the on-device sampler over the head logits; it leaves its choice in the argmax partials
+hipError_t launch_sampler(llm_model *m) {
+    SampleArgs a;
+    memset(&a, 0, sizeof a);
+    a.logits = m->logits;
+    a.n = m->info.n_logits;
+    a.probs = m->smp_p;
+    a.key[0] = m->smp_key;
+    a.key[1] = m->smp_key + a.n;
+    a.idx[0] = m->smp_idx;
+    a.idx[1] = m->smp_idx + a.n;
+    a.ss = m->ss;
+    a.ctrl = m->ctrl;
+    a.pv = m->part_v;
+    a.pi = m->part_i;
+    a.np = m->s_head.grid;
+    return launch_sample(a, m->st);
+}
+
+// Enqueue one decode step on m->st.  prof != NULL records events around every launch.  Kernel kinds whose
+// bit is set in `skip` are left out (the in-graph timing of llm_profile_graph compares such steps).  With
+// `sampled`, the sampler follows the head.
+int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finalize, unsigned skip = 0,
+                 bool sampled = false) {
     const llm_info &I = m->info;
     const int dim = I.dim, kv = m->kv_dim;
     auto mark = [&](int kind, double bytes) {
@@ -180,9 +227,12 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
     e.np = m->s_head.grid;
     e.head_ids = m->head_ids_d;
     e.gen = m->gen;
-    mark(K_EMBED, dim + dim / m->gs * (m->emb_sf32 ? 4.0 : 2.0) + dim * 4.0);
-    HIP_OR_FAIL("llm", launch_embed(e, m->st));
-    done();
+    auto on = [&](int kind) { return !(skip & (1u << kind)); };
+    if (on(K_EMBED)) {
+        mark(K_EMBED, kind_bytes(m, K_EMBED, pos_hint));
+        HIP_OR_FAIL("llm", launch_embed(e, m->st));
+        done();
+    }
 
     for (int l = 0; l < I.n_layers; l++) {
         const Layer &Ly = m->L[l];
@@ -205,9 +255,11 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
             fprintf(stderr, "llm: internal error: Qwen layer %d has no bias table\n", l);
             return -1;
         }
-        mark(K_QKV, gemv_algo_bytes(Ly.qkv.rows, dim, wb, m->gs, sf));
-        HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_NORM, EPI_QKV, a, Ly.s_qkv.grid, m->st));
-        done();
+        if (on(K_QKV)) {
+            mark(K_QKV, kind_bytes(m, K_QKV, pos_hint));
+            HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_NORM, EPI_QKV, a, Ly.s_qkv.grid, m->st));
+            done();
+        }
 
         AttnArgs t;
         t.q = m->q;
@@ -222,9 +274,11 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         t.splits = m->att_splits;
         t.max_pos = m->ctx;
         t.ctrl = m->ctrl;
-        mark(K_ATTN, attn_bytes(m, pos_hint));
-        HIP_OR_FAIL("llm", launch_attention(t, m->st));
-        done();
+        if (on(K_ATTN)) {
+            mark(K_ATTN, kind_bytes(m, K_ATTN, pos_hint));
+            HIP_OR_FAIL("llm", launch_attention(t, m->st));
+            done();
+        }
 
         a = base_args(m, Ly.o, Ly.s_o);
         a.att_ml = m->att_ml;
@@ -233,9 +287,11 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         a.head_size = m->hs;
         a.att_splits = m->att_splits;
         a.out = m->x;
-        mark(K_O, gemv_algo_bytes(dim, dim, wb, m->gs, sf));
-        HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_ATTN, EPI_RESID, a, Ly.s_o.grid, m->st));
-        done();
+        if (on(K_O)) {
+            mark(K_O, kind_bytes(m, K_O, pos_hint));
+            HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_ATTN, EPI_RESID, a, Ly.s_o.grid, m->st));
+            done();
+        }
 
         a = base_args(m, Ly.gu, Ly.s_gu);
         a.x = m->x;
@@ -243,35 +299,42 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         a.hq = m->hq;
         a.hs = m->hsc;
         a.dim = I.hidden_dim; // SwiGLU epilogue: number of hidden values
-        mark(K_GU, gemv_algo_bytes(Ly.gu.rows, dim, wb, m->gs, sf));
-        HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_NORM, EPI_SWIGLU, a, Ly.s_gu.grid, m->st));
-        done();
+        if (on(K_GU)) {
+            mark(K_GU, kind_bytes(m, K_GU, pos_hint));
+            HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_NORM, EPI_SWIGLU, a, Ly.s_gu.grid, m->st));
+            done();
+        }
 
         a = base_args(m, Ly.down, Ly.s_down);
         a.xq = m->hq;
         a.xs = m->hsc;
         a.out = m->x;
-        mark(K_DOWN, gemv_algo_bytes(dim, I.hidden_dim, wb, m->gs, sf));
-        HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_XQ, EPI_RESID, a, Ly.s_down.grid, m->st));
-        done();
+        if (on(K_DOWN)) {
+            mark(K_DOWN, kind_bytes(m, K_DOWN, pos_hint));
+            HIP_OR_FAIL("llm", launch_gemv(wb, m->gs, sf, PRO_XQ, EPI_RESID, a, Ly.s_down.grid, m->st));
+            done();
+        }
     }
 
-    mark(K_HEAD, gemv_algo_bytes(m->head.rows, dim, 8, m->gs, m->head.sf32));
-    HIP_OR_FAIL("llm", launch_head(m, hist));
-    done();
+    if (on(K_HEAD)) {
+        mark(K_HEAD, kind_bytes(m, K_HEAD, pos_hint));
+        HIP_OR_FAIL("llm", launch_head(m, hist));
+        done();
+    }
+    if (sampled) HIP_OR_FAIL("llm", launch_sampler(m));
 
     if (finalize) { // the step's own argmax; in a captured sequence the next step's start kernel does it
-        mark(K_ARGMAX, m->s_head.grid * 8.0);
+        mark(K_ARGMAX, kind_bytes(m, K_ARGMAX, pos_hint));
         HIP_OR_FAIL("llm", launch_finalize(m));
         done();
     }
     return 0;
 }
 
-int capture(llm_model *m, bool hist, hipGraphExec_t *out) {
+int capture(llm_model *m, bool hist, hipGraphExec_t *out, unsigned skip = 0, bool sampled = false) {
     hipGraph_t g;
     HIP_OR_FAIL("llm", hipStreamBeginCapture(m->st, hipStreamCaptureModeThreadLocal));
-    int rc = enqueue_step(m, hist, nullptr, 0, false);
+    int rc = enqueue_step(m, hist, nullptr, 0, false, skip, sampled);
     hipError_t e = hipStreamEndCapture(m->st, &g);
     if (rc || e != hipSuccess) {
         fprintf(stderr, "llm: graph capture failed: %s\n", hipGetErrorString(e));
@@ -804,7 +867,7 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
 
 // All n prompt positions, then the head of the last one: logits, argmax partials, and (finalize) its argmax
 // into gen[n - 1].  Afterwards the step state is position n - 1, as after n forward() calls.
-int prefill_all(llm_model *m, const int *ids, int n) {
+int prefill_all(llm_model *m, const int *ids, int n, bool sampled = false) {
     if (prefill_alloc(m, std::min(n, PREFILL_CHUNK))) return -1;
     for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
         const int M = std::min(PREFILL_CHUNK, n - p0);
@@ -816,14 +879,15 @@ int prefill_all(llm_model *m, const int *ids, int n) {
     HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->tokens, ids, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
     if (set_ctrl(m, n - 1, ids[n - 1], 0, 0)) return -1;
     HIP_OR_FAIL("llm_prefill", launch_head(m, false));
+    if (sampled) HIP_OR_FAIL("llm_prefill", launch_sampler(m));
     HIP_OR_FAIL("llm_prefill", launch_finalize(m));
     return 0;
 }
 
 void free_model(llm_model *m) {
     if (m->st) hipStreamSynchronize(m->st);
-    if (m->g_plain) hipGraphExecDestroy(m->g_plain);
-    if (m->g_hist) hipGraphExecDestroy(m->g_hist);
+    for (hipGraphExec_t g : {m->g_plain, m->g_hist, m->g_plain_s, m->g_hist_s})
+        if (g) hipGraphExecDestroy(g);
     for (void *p : m->allocs) hipFree(p);
     if (m->hist) hipFree(m->hist);
     for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
@@ -935,15 +999,15 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
             return -1;
         }
     hipSetDevice(m->device);
-    const bool hist = logits != nullptr;
-    hipGraphExec_t *g = hist ? &m->g_hist : &m->g_plain;
+    const bool hist = logits != nullptr, smp = m->sampling;
+    hipGraphExec_t *g = smp ? (hist ? &m->g_hist_s : &m->g_plain_s) : (hist ? &m->g_hist : &m->g_plain);
     if (hist && !m->hist) {
         if (hipMalloc(&m->hist, (size_t)m->ctx * m->info.n_logits * 4) != hipSuccess) {
             fprintf(stderr, "llm_generate: no room for the logits history\n");
             return -1;
         }
     }
-    if (!*g && capture(m, hist, g)) return -1;
+    if (!*g && capture(m, hist, g, 0, smp)) return -1;
     HIP_OR_FAIL("llm_generate", hipMemcpy(m->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
     if (set_ctrl(m, -1, 0, n_prompt, 1)) return -1;
     // positions: the prompt, then one per generated token, within the context
@@ -951,7 +1015,7 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
     const double t0 = now_ms();
     if (m->prefill_on && !hist && n_prompt > 1) {
         // the prompt in one batched pass; the first decode step then finishes its last position's argmax
-        if (prefill_all(m, prompt, n_prompt)) return -1;
+        if (prefill_all(m, prompt, n_prompt, smp)) return -1;
         if (set_ctrl(m, n_prompt - 1, prompt[n_prompt - 1], n_prompt, 1)) return -1;
     } else {
         for (int p = 0; p < n_prompt; p++) HIP_OR_FAIL("llm_generate", hipGraphLaunch(*g, m->st));
@@ -1069,6 +1133,81 @@ extern "C" int llm_profile(llm_model *m, int steps, llm_kernel_stat *stats, int 
     return n;
 }
 
+// In-graph kernel times: the step graph is replayed `steps` times from the current position, then once per
+// kernel kind with that kind's launches left out; the difference is that kind's time inside the replayed
+// graph (its duration plus its share of the gaps between graph nodes), so launch and event overheads of
+// eager timing do not enter it.  Each variant runs `rounds` times, alternating with the full step, and the
+// medians are used.  The step control (position, token) is restored at the end.
+extern "C" int llm_profile_graph(llm_model *m, int steps, int rounds, llm_kernel_stat *stats, int max_stats,
+                                 double *step_ms) {
+    if (!m || steps < 1 || rounds < 1 || !stats) return -1;
+    hipSetDevice(m->device);
+    StepCtrl saved, c;
+    HIP_OR_FAIL("llm_profile_graph", hipMemcpy(&saved, m->ctrl, sizeof saved, hipMemcpyDeviceToHost));
+    if (saved.pos + steps >= m->ctx) {
+        fprintf(stderr, "llm_profile_graph: %d steps from position %d do not fit the context %d\n", steps, saved.pos,
+                m->ctx);
+        return -1;
+    }
+    c = saved;
+    c.mode = 1;
+    c.n_prompt = 0;
+    const int kinds[] = {K_EMBED, K_QKV, K_ATTN, K_O, K_GU, K_DOWN, K_HEAD};
+    const int nk = sizeof kinds / sizeof kinds[0];
+    const int per_step[] = {1, m->info.n_layers, m->info.n_layers, m->info.n_layers, m->info.n_layers,
+                            m->info.n_layers, 1};
+    std::vector<hipGraphExec_t> g(nk + 1, nullptr);
+    int rc = capture(m, false, &g[nk]);
+    for (int k = 0; k < nk && !rc; k++) rc = capture(m, false, &g[k], 1u << kinds[k]);
+    hipEvent_t e0, e1;
+    hipEventCreate(&e0);
+    hipEventCreate(&e1);
+    auto run = [&](hipGraphExec_t ge, double *ms) -> int {
+        HIP_OR_FAIL("llm_profile_graph", hipMemcpyAsync(m->ctrl, &c, sizeof c, hipMemcpyHostToDevice, m->st));
+        hipEventRecord(e0, m->st);
+        for (int i = 0; i < steps; i++) HIP_OR_FAIL("llm_profile_graph", hipGraphLaunch(ge, m->st));
+        hipEventRecord(e1, m->st);
+        HIP_OR_FAIL("llm_profile_graph", hipEventSynchronize(e1));
+        float t = 0;
+        hipEventElapsedTime(&t, e0, e1);
+        *ms = t;
+        return 0;
+    };
+    std::vector<std::vector<double>> full(nk), part(nk);
+    if (!rc && run(g[nk], step_ms)) rc = -1; // warm-up
+    for (int r = 0; r < rounds && !rc; r++)
+        for (int k = 0; k < nk && !rc; k++) {
+            double a = 0, b = 0;
+            if (run(g[nk], &a) || run(g[k], &b)) rc = -1;
+            full[k].push_back(a);
+            part[k].push_back(b);
+        }
+    for (hipGraphExec_t ge : g)
+        if (ge) hipGraphExecDestroy(ge);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (hipMemcpy(m->ctrl, &saved, sizeof saved, hipMemcpyHostToDevice) != hipSuccess) rc = -1;
+    if (rc) return -1;
+    auto median = [](std::vector<double> v) {
+        std::sort(v.begin(), v.end());
+        return v[v.size() / 2];
+    };
+    std::vector<double> all;
+    int n = 0;
+    for (int k = 0; k < nk && n < max_stats; k++) {
+        const double tf = median(full[k]), tp = median(part[k]);
+        all.insert(all.end(), full[k].begin(), full[k].end());
+        memset(&stats[n], 0, sizeof stats[n]);
+        snprintf(stats[n].name, sizeof stats[n].name, "%s", k_names[kinds[k]]);
+        stats[n].launches = per_step[k] * steps;
+        stats[n].total_ms = tf - tp;
+        stats[n].bytes_per_launch = kind_bytes(m, kinds[k], saved.pos + 1 + steps / 2);
+        n++;
+    }
+    if (step_ms) *step_ms = median(all) / steps;
+    return n;
+}
+
 extern "C" int llm_read_state(llm_model *m, int which, int layer, float *dst, size_t count) {
     if (!m || !dst) return -1;
     hipSetDevice(m->device);
@@ -1100,6 +1239,33 @@ extern "C" int llm_prefill(llm_model *m, const int *ids, int n, float *logits) {
         HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(logits, m->logits, (size_t)m->info.n_logits * 4,
                                                   hipMemcpyDeviceToHost, m->st));
     HIP_OR_FAIL("llm_prefill", hipStreamSynchronize(m->st));
+    return 0;
+}
+
+extern "C" int llm_set_sampler(llm_model *m, float temperature, float topp, unsigned long long seed) {
+    if (!m) return -1;
+    hipSetDevice(m->device);
+    HIP_OR_FAIL("llm_set_sampler", hipStreamSynchronize(m->st));
+    const size_t n = (size_t)m->info.n_logits;
+    if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4) ||
+                   dalloc(m, &m->smp_key, 2 * n * 4) || dalloc(m, &m->smp_idx, 2 * n * 4)))
+        return -1;
+    SamplerState st;
+    st.temperature = temperature;
+    st.topp = topp;
+    st.rng = seed;
+    HIP_OR_FAIL("llm_set_sampler", hipMemcpy(m->ss, &st, sizeof st, hipMemcpyHostToDevice));
+    m->sampling = temperature > 0.0f; // the reference samples unless the temperature is 0 (qwen.c:647)
+    return 0;
+}
+
+extern "C" int llm_sampler_state(llm_model *m, unsigned long long *rng) {
+    if (!m || !rng) return -1;
+    if (!m->ss) { *rng = 0; return 0; }
+    hipSetDevice(m->device);
+    SamplerState st;
+    HIP_OR_FAIL("llm_sampler_state", hipMemcpy(&st, m->ss, sizeof st, hipMemcpyDeviceToHost));
+    *rng = st.rng;
     return 0;
 }
 

@@ -283,9 +283,14 @@ unsigned int or_random_u32(unsigned long long *state) {
 float or_random_f32(unsigned long long *state) { return (or_random_u32(state) >> 8) / 16777216.0f; }
 
 typedef struct { float p; int i; } or_pi;
+/* qwen.c:609-614 orders by probability only; C leaves the order of equal keys to qsort, and glibc's qsort
+ * (a merge sort while the array fits in memory) keeps them in their input order, i.e. ascending index.  The
+ * index tie-break states that order explicitly. */
 static int by_prob_desc(const void *a, const void *b) {
     float x = ((const or_pi *)a)->p, y = ((const or_pi *)b)->p;
-    return x > y ? -1 : x < y ? 1 : 0;
+    if (x != y) return x > y ? -1 : 1;
+    int i = ((const or_pi *)a)->i, j = ((const or_pi *)b)->i;
+    return i < j ? -1 : i > j ? 1 : 0;
 }
 
 int or_sample(float *logits, int n, float temperature, float topp, unsigned long long *rng) {

@@ -13,6 +13,15 @@ void refq_rmsnorm(float *o, const float *x, const float *w, int n, float eps) { 
 void refq_softmax(float *x, int n) { softmax(x, n); }                                  /* qwen.c:346-352 */
 void refq_rope(float *v, int n_heads, int hs, const float *c, const float *s) { rope(v, n_heads, hs, c, s); } /* 478-488 */
 int refq_argmax(const float *p, int n) { return sample_argmax(p, n); }                /* qwen.c:591-598 */
+/* sample (qwen.c:647-654) with a Sampler of caller settings; *rng in and out */
+int refq_sample(float *logits, int n, float temperature, float topp, unsigned long long *rng) {
+    Sampler s = { .vocab_size = n, .temperature = temperature, .topp = topp, .rng_state = *rng,
+                  .probindex = malloc((size_t)n * sizeof(ProbIndex)) };
+    int r = sample(&s, logits);
+    *rng = s.rng_state;
+    free(s.probindex);
+    return r;
+}
 
 /* matmul_cpu (qwen.c:407-457) on caller-owned planes */
 void refq_matmul(float *out, const uint8_t *w, const uint16_t *s, int n, int d, int bits, const int8_t *xq,

@@ -6,7 +6,8 @@ Run from the repository root after `make -C oracle all ref` and `make -C local-l
 The reference's tests hold no golden vectors (its checks compare the FPGA kernel with the CPU function on
 the fly), so every expected output here comes from running the reference code itself:
   - tiny.qwb / tiny.bin: seeded synthetic models (host/synth), small enough to commit,
-  - *_ref.logits / *_ref.json: the reference binaries' --logits dump and greedy ids on those models,
+  - *_ref.logits / *_ref.json: the reference binaries' --logits dump, greedy ids and sampled ids (temperature,
+    top-p or the plain cdf walk, seeded xorshift coin) on those models,
   - ops.npz: the reference's quantize() and matmul() (qwen.c and runq.c, through oracle/_ref/libref_*.so)
     on seeded inputs, crafted edge groups and the reference testbench's special fp16 scales.
 """
@@ -65,9 +66,17 @@ def main():
                     "0.9", "-s", "42", "-n", "20", "-c", "64"])
     out["qwb_sampled"] = {"prompt": QWEN_PROMPT, "ids": [int(v) for v in ids.split(",")], "n": 20, "ctx": 64,
                           "t": 0.9, "p": 0.9, "seed": 42}
+    ids, err = run([os.path.join(REF, "qwen"), tq, "--ids", ",".join(map(str, QWEN_PROMPT)), "-t", "1.0", "-p",
+                    "1.0", "-s", "7", "-n", "20", "-c", "64"])
+    out["qwb_sampled_mult"] = {"prompt": QWEN_PROMPT, "ids": [int(v) for v in ids.split(",")], "n": 20, "ctx": 64,
+                               "t": 1.0, "p": 1.0, "seed": 7}
     ids, err = run([os.path.join(REF, "runq_ids"), tb, "--ids", ",".join(map(str, BIN_PROMPT)), "-n", "32",
                     "--logits", os.path.join(HERE, "tiny_bin_ref.logits")])
     out["bin"] = {"prompt": BIN_PROMPT, "ids": [int(v) for v in ids.split(",")], "steps": 32}
+    ids, err = run([os.path.join(REF, "runq_ids"), tb, "--ids", ",".join(map(str, BIN_PROMPT)), "-n", "32",
+                    "-t", "0.8", "-p", "0.9", "-s", "5"])
+    out["bin_sampled"] = {"prompt": BIN_PROMPT, "ids": [int(v) for v in ids.split(",")], "steps": 32,
+                          "t": 0.8, "p": 0.9, "seed": 5}
     with open(os.path.join(HERE, "tiny_ref.json"), "w") as f:
         json.dump(out, f, indent=1)
 

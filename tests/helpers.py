@@ -57,6 +57,8 @@ def oracle():
         L.or_argmax.argtypes = [vp, i32]
         L.or_random_u32.restype = C.c_uint
         L.or_random_u32.argtypes = [C.POINTER(C.c_ulonglong)]
+        L.or_random_f32.restype = C.c_float
+        L.or_random_f32.argtypes = [C.POINTER(C.c_ulonglong)]
         L.or_sample.argtypes = [vp, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong)]
         L.or_open.restype = vp
         L.or_open.argtypes = [C.c_char_p, i32]

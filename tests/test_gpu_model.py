@@ -127,9 +127,10 @@ def test_runq_c1_shape(tmp_path):
                                    ("dim=256", "heads=2", "kv_heads=1")])
 def test_decode_attention_at_long_context(tmp_path, shape):
     """head sizes 32/64/128: positions 4000..4095 decoded after a 4000-token prefill.  A 4096-position cache
-    splits them into 64 slices of at most 64 positions (the one-wave-per-head register kernel); an
-    8192-position cache runs the same slices through the LDS-staged kernel.  Both hold bitwise the same
-    prefilled cache; both are held to the oracle's logits (flip-limited bar) and to each other."""
+    splits them into 64 slices of at most 64 positions (the short-slice kernel: one round of loads, a wave
+    per query head); an 8192-position cache runs the same slices through the sub-chunked online-softmax
+    kernel.  Both hold bitwise the same prefilled cache; both are held to the oracle's logits (flip-limited
+    bar) and to each other."""
     n0, n1 = 4000, 4096
     p = synth("qwb", str(tmp_path / "long.qwb"), "tiny", 41, "layers=1", "max_seq=8192", *shape)
     om = OracleModel(p, n1)
@@ -157,6 +158,24 @@ def test_decode_replay_and_profile_run():
     names = {s["name"] for s in st}
     assert {"step_start", "qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv"} <= names
     m.close()
+
+
+def test_in_graph_profile_accounts_for_the_step_and_restores_the_position():
+    """llm_profile_graph: one record per kernel kind, the kinds' in-graph times add up to about the replayed
+    step, and the step control is restored (a later generate still reproduces the reference ids)"""
+    m = pkg().Model(os.path.join(GOLDEN, "tiny.qwb"), 64)
+    meta = META["qwb"]
+    m.generate(meta["prompt"], 2)
+    st, step_ms = m.profile_graph(8, 3)
+    names = [s["name"] for s in st]
+    assert names == ["step_start", "qkv_gemv", "attention", "o_gemv", "gateup_gemv", "down_gemv", "head_gemv"]
+    by = {s["name"]: s for s in st}
+    assert by["qkv_gemv"]["launches"] == 8 * m.info.n_layers and by["head_gemv"]["launches"] == 8
+    total = sum(s["total_ms"] for s in st) / 8
+    assert step_ms > 0 and 0.5 * step_ms < total < 1.5 * step_ms, (total, step_ms, st)
+    r = m.generate(meta["prompt"], meta["n"])
+    m.close()
+    assert list(r["ids"]) == meta["ids"]
 
 
 def test_positions_beyond_context_are_rejected(capfd):

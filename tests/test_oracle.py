@@ -251,25 +251,50 @@ def test_whole_model_bin_matches_reference_bit_exactly():
     m.close()
 
 
-def test_sampler_matches_reference_stream():
-    """temperature + top-p with the xorshift coin: the reference binary's sampled ids (-t 0.9 -p 0.9 -s 42)"""
-    meta = json.load(open(os.path.join(GOLDEN, "tiny_ref.json")))["qwb_sampled"]
-    m = OracleModel(os.path.join(GOLDEN, "tiny.qwb"), meta["ctx"])
+@pytest.mark.parametrize("name", ["qwb_sampled", "qwb_sampled_mult", "bin_sampled"])
+def test_sampler_matches_reference_stream(name):
+    """temperature + top-p (or the plain cdf walk at topp 1) with the xorshift coin: the reference binaries'
+    sampled ids (qwen -t 0.9 -p 0.9 -s 42 and -t 1 -p 1 -s 7; runq -t 0.8 -p 0.9 -s 5)"""
+    meta = json.load(open(os.path.join(GOLDEN, "tiny_ref.json")))[name]
+    runq = name.startswith("bin")
+    m = OracleModel(os.path.join(GOLDEN, "tiny.bin" if runq else "tiny.qwb"), 0 if runq else meta["ctx"])
     rng = C.c_ulonglong(meta["seed"])
     token, out = meta["prompt"][0], []
-    for pos in range(meta["ctx"]):
+    for pos in range(meta["steps"] if runq else meta["ctx"]):
         lg = m.forward(token, pos)
         if pos < len(meta["prompt"]) - 1:
             token = meta["prompt"][pos + 1]
             continue
         row = oracle().or_sample(ptr(lg), m.n, C.c_float(meta["t"]), C.c_float(meta["p"]), C.byref(rng))
         nxt = int(m.head_ids[row])
+        if runq and nxt == 1:  # runq stops at BOS (runq.c:1016)
+            break
         out.append(nxt)
-        if len(out) >= meta["n"]:
+        if not runq and len(out) >= meta["n"]:
             break
         token = nxt
     m.close()
     assert out == meta["ids"]
+
+
+def test_sampler_matches_the_reference_sample_function():
+    """or_sample against the reference's own sample() (qwen.c:647-654 through oracle/_ref) on random, peaked
+    and tied logits, every mode: same rows and the same RNG state"""
+    ref = ref_lib("qwen")
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    rng = np.random.default_rng(77)
+    for n in (2, 300, 5000):
+        for scale in (0.05, 2.0, 12.0, -1.0):
+            for temp, topp in ((0.5, 0.0), (1.0, 0.5), (0.9, 0.9), (1.3, 0.99), (0.8, 1.0)):
+                lg = rng.standard_normal(n).astype(np.float32) * abs(scale)
+                if scale < 0:
+                    lg = np.round(lg * 2)  # ties
+                a, b = lg.copy(), lg.copy()
+                sa, sb = C.c_ulonglong(1234 + n), C.c_ulonglong(1234 + n)
+                ra = oracle().or_sample(ptr(a), n, C.c_float(temp), C.c_float(topp), C.byref(sa))
+                rb = ref.refq_sample(ptr(b), n, C.c_float(temp), C.c_float(topp), C.byref(sb))
+                assert (ra, sa.value) == (rb, sb.value), (n, scale, temp, topp)
 
 
 def test_xorshift_first_values():
