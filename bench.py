@@ -247,6 +247,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--cpu-tokens", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sample", default=None, metavar="T,P,SEED",
+                    help="decode with the on-device sampler (temperature, top-p, seed) instead of the argmax")
     ap.add_argument("--calib", action="store_true", help="run the counter calibration copy first")
     ap.add_argument("--counters", action="store_true",
                     help="counter pass: the calibration copy, then the prompt and --profile-steps decode steps as "
@@ -299,6 +301,14 @@ def main():
     log(f"greedy run: {len(ids_gpu)} tokens, device decode {gen['timing'].decode_ms:.1f} ms "
         f"({(gen['timing'].n_forward - len(prompt)) / gen['timing'].decode_ms * 1e3:.0f} tok/s with host stop checks)")
 
+    # --sample: the timed steps draw with the on-device sampler (the greedy run above stays the parity line)
+    decoding = "argmax"
+    if a.sample:
+        t_, p_, s_ = a.sample.split(",")
+        m.set_sampler(float(t_), float(p_), int(s_))
+        decoding = f"sampler temperature {float(t_)} top-p {float(p_)} seed {int(s_)}"
+        log(f"decoding with the on-device {decoding}")
+
     # warmup: W steps after the prompt, then back to the prompt's end for the timed steps
     m.generate(prompt, 1)
     if a.warmup:
@@ -315,6 +325,7 @@ def main():
     # per-kernel roofline: each kernel kind's time inside the replayed step graph (HIP events around graph
     # replays with and without that kind's launches, on the library's stream); eager per-launch event times,
     # which add launch and event overhead to every kernel, are logged beside them
+    m.set_sampler(0.0)  # the per-kernel figures are those of the argmax step
     m.generate(prompt, 1)
     eager = {s["name"]: s for s in m.profile(a.profile_steps)}
     m.generate(prompt, 1)
@@ -352,6 +363,7 @@ def main():
         "data": "synthetic: seeded N(0,0.02) random-init weights (" + ("Q4_0 layers, Q8_0 head" if cfg["fmt"] == "qwb"
                  else "Q8_0 with fp32 scales") + "), seeded prompt ids",
         "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
+                   "decoding": decoding,
                    "ctx": ctx_used, "batch": 1},
         "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),

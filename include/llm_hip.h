@@ -61,7 +61,8 @@ int llm_generate(llm_model *m, const int *prompt, int n_prompt, int max_new, int
 
 /* Decode throughput: replays the captured step graph `steps` times from the current position (after a
  * prompt was forced by llm_generate or llm_forward) with no host round trips, and returns the elapsed time
- * of exactly those replays in *ms (HIP events on the library's stream). */
+ * of exactly those replays in *ms (HIP events on the library's stream).  With the sampler on
+ * (llm_set_sampler, temperature > 0) the replayed steps draw their tokens with it. */
 int llm_decode_replay(llm_model *m, int steps, double *ms);
 
 /* Per-kernel timing of decode steps: runs `steps` steps with HIP events around every launch (on the

@@ -154,30 +154,25 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     }
     if (hook_device("mvh_sample")) return -1;
     float *dl = nullptr, *dp = nullptr;
-    unsigned *dk = nullptr;
-    int *di = nullptr, *dr = nullptr;
+    int *dr = nullptr;
     SamplerState *dss = nullptr;
     SamplerState st;
     st.temperature = temperature;
     st.topp = topp;
     st.rng = *rng;
     int rc = -1;
-    if (hipMalloc(&dl, (size_t)count * n * 4) == hipSuccess && hipMalloc(&dp, (size_t)n * 4) == hipSuccess &&
-        hipMalloc(&dk, (size_t)2 * n * 4) == hipSuccess && hipMalloc(&di, (size_t)2 * n * 4) == hipSuccess &&
+    const size_t ld = ((size_t)n + 3) & ~(size_t)3; // 16-byte aligned rows
+    if (hipMalloc(&dl, (size_t)count * ld * 4) == hipSuccess && hipMalloc(&dp, (size_t)n * 4) == hipSuccess &&
         hipMalloc(&dr, (size_t)count * 4) == hipSuccess && hipMalloc(&dss, sizeof st) == hipSuccess &&
-        hipMemcpy(dl, logits, (size_t)count * n * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy2D(dl, ld * 4, logits, (size_t)n * 4, (size_t)n * 4, count, hipMemcpyHostToDevice) == hipSuccess &&
         hipMemcpy(dss, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess) {
         rc = 0;
         for (int c = 0; c < count && !rc; c++) {
             SampleArgs a;
             memset(&a, 0, sizeof a);
-            a.logits = dl + (size_t)c * n;
+            a.logits = dl + (size_t)c * ld;
             a.n = n;
             a.probs = dp;
-            a.key[0] = dk;
-            a.key[1] = dk + n;
-            a.idx[0] = di;
-            a.idx[1] = di + n;
             a.ss = dss;
             a.out_row = dr + c;
             if (launch_sample(a, 0) != hipSuccess) rc = -1;
@@ -191,8 +186,6 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     else *rng = st.rng;
     hipFree(dl);
     hipFree(dp);
-    hipFree(dk);
-    hipFree(di);
     hipFree(dr);
     hipFree(dss);
     return rc;

@@ -118,8 +118,6 @@ struct SampleArgs {
     const float *logits;    // [n] head logits
     int n;
     float *probs;           // [n] scratch: probabilities
-    unsigned *key[2];       // [n] each: candidate sort keys (ping-pong)
-    int *idx[2];            // [n] each: candidate rows
     SamplerState *ss;
     const StepCtrl *ctrl;   // generate mode: no draw while the next token is a prompt token; NULL: always draw
     float *pv;              // [np] argmax partials of the step: the choice becomes the only finite entry

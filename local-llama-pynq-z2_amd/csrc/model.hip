@@ -76,8 +76,6 @@ struct llm_model {
     bool sampling = false;
     SamplerState *ss = nullptr;
     float *smp_p = nullptr;
-    unsigned *smp_key = nullptr;
-    int *smp_idx = nullptr;
     hipGraphExec_t g_plain_s = nullptr, g_hist_s = nullptr;
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, prefill_on = 1;
@@ -175,10 +173,6 @@ hipError_t launch_sampler(llm_model *m) {
     a.logits = m->logits;
     a.n = m->info.n_logits;
     a.probs = m->smp_p;
-    a.key[0] = m->smp_key;
-    a.key[1] = m->smp_key + a.n;
-    a.idx[0] = m->smp_idx;
-    a.idx[1] = m->smp_idx + a.n;
     a.ss = m->ss;
     a.ctrl = m->ctrl;
     a.pv = m->part_v;
@@ -989,7 +983,7 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
         fprintf(stderr, "llm_generate: bad arguments\n");
         return -1;
     }
-    if (n_prompt >= m->ctx) {
+    if (n_prompt > m->ctx) { // a prompt of exactly ctx positions still yields one token from the last
         fprintf(stderr, "prompt (%d tokens) does not fit -c %d\n", n_prompt, m->ctx);
         return -1;
     }
@@ -1074,12 +1068,13 @@ extern "C" int llm_decode_replay(llm_model *m, int steps, double *ms) {
     c.mode = 1;
     c.n_prompt = 0;
     HIP_OR_FAIL("llm_decode_replay", hipMemcpy(m->ctrl, &c, sizeof c, hipMemcpyHostToDevice));
-    if (!m->g_plain && capture(m, false, &m->g_plain)) return -1;
+    hipGraphExec_t *g = m->sampling ? &m->g_plain_s : &m->g_plain;
+    if (!*g && capture(m, false, g, 0, m->sampling)) return -1;
     hipEvent_t e0, e1;
     hipEventCreate(&e0);
     hipEventCreate(&e1);
     hipEventRecord(e0, m->st);
-    for (int i = 0; i < steps; i++) HIP_OR_FAIL("llm_decode_replay", hipGraphLaunch(m->g_plain, m->st));
+    for (int i = 0; i < steps; i++) HIP_OR_FAIL("llm_decode_replay", hipGraphLaunch(*g, m->st));
     hipEventRecord(e1, m->st);
     HIP_OR_FAIL("llm_decode_replay", hipEventSynchronize(e1));
     float t = 0;
@@ -1247,9 +1242,7 @@ extern "C" int llm_set_sampler(llm_model *m, float temperature, float topp, unsi
     hipSetDevice(m->device);
     HIP_OR_FAIL("llm_set_sampler", hipStreamSynchronize(m->st));
     const size_t n = (size_t)m->info.n_logits;
-    if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4) ||
-                   dalloc(m, &m->smp_key, 2 * n * 4) || dalloc(m, &m->smp_idx, 2 * n * 4)))
-        return -1;
+    if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4))) return -1;
     SamplerState st;
     st.temperature = temperature;
     st.topp = topp;

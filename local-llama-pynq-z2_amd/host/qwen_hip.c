@@ -2,10 +2,11 @@
  * libmatvec_hip.so's device-resident API.  Same options and output as qwen.c for token-id prompts:
  *   qwen_hip model.qwb --ids a,b,c [-t temp] [-p topp] [-s seed] [-n new] [-c ctx] [--logits file]
  * stdout: generated ids, comma separated (qwen.c:696); stderr: the prompt/generation rate line (709-711).
- * -t 0 runs the whole loop on the device (hipGraph per token, argmax on the device); -t > 0 copies each
- * position's logits to the host for the reference's sampler.  Text prompts need the tokenizer, which this
- * host does not carry: give token ids. */
+ * The whole loop runs on the device (hipGraph per token): the argmax at -t 0, the reference's sampler
+ * (temperature, top-p, xorshift coin; qwen.c:578-654) at -t > 0.  Text prompts need the tokenizer, which
+ * this host does not carry: give token ids. */
 #include <stdint.h>
+#include <time.h>
 
 #include "hostcli.h"
 #include "llm_hip.h"
@@ -52,47 +53,20 @@ int main(int argc, char **argv) {
     if (n_ids >= info.ctx) { fprintf(stderr, "prompt (%d tokens) does not fit -c %d\n", n_ids, info.ctx); return 1; }
     FILE *dump = NULL;
     if (logits_path && !(dump = fopen(logits_path, "wb"))) { fprintf(stderr, "cannot write %s\n", logits_path); return 1; }
-    const int32_t *head_ids = llm_head_ids(m);
-    int n_gen = 0, n_fwd_gen = 0;
-    double prompt_s, gen_s;
-    if (temperature == 0.0f) {
-        int *out = calloc(steps, sizeof(int));
-        float *lg = NULL;
-        if (dump) lg = malloc((size_t)(n_ids + steps) * info.n_logits * sizeof(float));
-        llm_timing t;
-        n_gen = llm_generate(m, ids, n_ids, steps, out, lg, &t);
-        if (n_gen < 0) return 1;
-        for (int i = 0; i < n_gen; i++) printf(i ? ",%d" : "%d", out[i]);
-        if (dump) fwrite(lg, sizeof(float), (size_t)t.n_forward * info.n_logits, dump);
-        n_fwd_gen = t.n_forward - n_ids;
-        prompt_s = t.prompt_ms / 1000.0;
-        gen_s = t.decode_ms / 1000.0;
-        if (t.n_forward == info.ctx && n_gen < steps) fprintf(stderr, "\n(context of %d tokens full)", info.ctx);
-        free(out);
-        free(lg);
-    } else { /* qwen.c:669-712 with the host sampler */
-        HostSampler s = {info.n_logits, temperature, topp, seed, malloc(sizeof(HostProb) * info.n_logits)};
-        float *lg = malloc(sizeof(float) * info.n_logits);
-        long start = now_ms(), prompt_done = start;
-        int token = ids[0], pos;
-        for (pos = 0; pos < info.ctx; pos++) {
-            if (llm_forward(m, token, pos, lg)) return 1;
-            if (dump) fwrite(lg, sizeof(float), info.n_logits, dump);
-            if (pos < n_ids - 1) { token = ids[pos + 1]; continue; }
-            if (pos == n_ids - 1) prompt_done = now_ms(); else n_fwd_gen++;
-            int next = head_ids[hs_sample(&s, lg)];
-            if (next == 151645 || next == 151643) break;
-            printf(n_gen ? ",%d" : "%d", next);
-            fflush(stdout);
-            if (++n_gen >= steps) break;
-            token = next;
-        }
-        long end = now_ms();
-        prompt_s = (prompt_done - start) / 1000.0;
-        gen_s = (end - prompt_done) / 1000.0;
-        free(lg);
-        free(s.buf);
-    }
+    if (llm_set_sampler(m, temperature, topp, seed)) return 1;
+    int *out = calloc(steps, sizeof(int));
+    float *lg = NULL;
+    if (dump) lg = malloc((size_t)(n_ids + steps) * info.n_logits * sizeof(float));
+    llm_timing t;
+    const int n_gen = llm_generate(m, ids, n_ids, steps, out, lg, &t);
+    if (n_gen < 0) return 1;
+    for (int i = 0; i < n_gen; i++) printf(i ? ",%d" : "%d", out[i]);
+    if (dump) fwrite(lg, sizeof(float), (size_t)t.n_forward * info.n_logits, dump);
+    const int n_fwd_gen = t.n_forward - n_ids;
+    const double prompt_s = t.prompt_ms / 1000.0, gen_s = t.decode_ms / 1000.0;
+    if (t.n_forward == info.ctx && n_gen < steps) fprintf(stderr, "\n(context of %d tokens full)", info.ctx);
+    free(out);
+    free(lg);
     printf("\n");
     fprintf(stderr, "prompt: %d tokens in %.2f s (%.2f tok/s); generated: %d tokens, %.2f tok/s\n", n_ids, prompt_s,
             n_ids / (prompt_s + 1e-12), n_gen, n_fwd_gen ? n_fwd_gen / (gen_s + 1e-12) : 0.0);

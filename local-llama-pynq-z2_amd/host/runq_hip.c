@@ -2,7 +2,8 @@
  * libmatvec_hip.so's device-resident API, for token-id prompts:
  *   runq_hip model.bin --ids a,b,c [-n steps] [-t temp] [-p topp] [-s seed] [--logits file]
  * -n counts positions including the prompt and is clamped to seq_len (runq.c:1200); generation stops at
- * BOS (1) (runq.c:1016).  stdout: generated ids; stderr: decode rate (tokens after the prompt / time). */
+ * BOS (1) (runq.c:1016).  The whole loop runs on the device: the argmax at -t 0, the reference's sampler
+ * (runq.c:830-967) at -t > 0.  stdout: generated ids; stderr: decode rate (tokens after the prompt / time). */
 #include <stdint.h>
 
 #include "hostcli.h"
@@ -38,42 +39,18 @@ int main(int argc, char **argv) {
     FILE *dump = NULL;
     if (logits_path && !(dump = fopen(logits_path, "wb"))) { fprintf(stderr, "cannot write %s\n", logits_path); return 1; }
     const int max_new = steps - n_ids + 1; /* positions n_ids-1 .. steps-1 each yield one token */
-    int n_gen = 0, n_fwd_gen = 0;
-    double gen_s = 0;
-    if (temperature == 0.0f && n_ids < info.ctx) {
-        int *out = calloc(max_new, sizeof(int));
-        float *lg = dump ? malloc((size_t)(n_ids + max_new) * info.n_logits * sizeof(float)) : NULL;
-        llm_timing t;
-        n_gen = llm_generate(m, ids, n_ids, max_new, out, lg, &t);
-        if (n_gen < 0) return 1;
-        for (int i = 0; i < n_gen; i++) printf(i ? ",%d" : "%d", out[i]);
-        if (dump) fwrite(lg, sizeof(float), (size_t)t.n_forward * info.n_logits, dump);
-        n_fwd_gen = t.n_forward - n_ids;
-        gen_s = t.decode_ms / 1000.0;
-        free(out);
-        free(lg);
-    } else { /* runq.c:982-1036 with the host sampler */
-        HostSampler s = {info.n_logits, temperature, topp, seed, malloc(sizeof(HostProb) * info.n_logits)};
-        float *lg = malloc(sizeof(float) * info.n_logits);
-        long prompt_done = now_ms();
-        int token = ids[0], pos = 0, next;
-        while (pos < steps) {
-            if (llm_forward(m, token, pos, lg)) return 1;
-            if (dump) fwrite(lg, sizeof(float), info.n_logits, dump);
-            if (pos < n_ids - 1) next = ids[pos + 1];
-            else {
-                if (pos == n_ids - 1) prompt_done = now_ms(); else n_fwd_gen++;
-                next = hs_sample(&s, lg);
-            }
-            pos++;
-            if (next == 1) break;
-            if (pos >= n_ids) { printf(n_gen ? ",%d" : "%d", next); n_gen++; }
-            token = next;
-        }
-        gen_s = (now_ms() - prompt_done) / 1000.0;
-        free(lg);
-        free(s.buf);
-    }
+    if (llm_set_sampler(m, temperature, topp, seed)) return 1;
+    int *out = calloc(max_new, sizeof(int));
+    float *lg = dump ? malloc((size_t)(n_ids + max_new) * info.n_logits * sizeof(float)) : NULL;
+    llm_timing t;
+    const int n_gen = llm_generate(m, ids, n_ids, max_new, out, lg, &t);
+    if (n_gen < 0) return 1;
+    for (int i = 0; i < n_gen; i++) printf(i ? ",%d" : "%d", out[i]);
+    if (dump) fwrite(lg, sizeof(float), (size_t)t.n_forward * info.n_logits, dump);
+    const int n_fwd_gen = t.n_forward - n_ids;
+    const double gen_s = t.decode_ms / 1000.0;
+    free(out);
+    free(lg);
     printf("\n");
     fprintf(stderr, "prompt: %d tokens; generated: %d tokens, %.2f tok/s\n", n_ids, n_gen,
             n_fwd_gen ? n_fwd_gen / (gen_s + 1e-12) : 0.0);

@@ -17,7 +17,7 @@ import subprocess
 import numpy as np
 import pytest
 
-from helpers import GOLDEN, REF_DIR, OracleModel, pkg, rel_err, synth
+from helpers import GOLDEN, PKG_DIR, REF_DIR, OracleModel, pkg, rel_err, synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -224,3 +224,29 @@ def test_reference_runq_host_on_the_dropin_library(tmp_path):
     assert np.array_equal(got, ref)
     line = [l for l in r.stderr.splitlines() if l.startswith("FPGA_CHECK")][0]
     assert "max abs diff 0," in line, line
+
+
+@pytest.mark.parametrize("name,extra", [("qwb", ["-t", "0"]), ("qwb_sampled", ["-t", "0.9", "-p", "0.9", "-s", "42"]),
+                                        ("qwb_sampled_mult", ["-t", "1.0", "-p", "1.0", "-s", "7"]),
+                                        ("bin", ["-t", "0"]), ("bin_sampled", ["-t", "0.8", "-p", "0.9", "-s", "5"])])
+def test_host_programs_match_reference_ids(name, extra, tmp_path):
+    """this package's C hosts (host/qwen_hip, host/runq_hip: the reference CLIs' token-id loop over the
+    device-resident API, argmax or the device sampler) against the reference binaries' ids; the greedy runs
+    also dump the reference's --logits file"""
+    meta = META[name]
+    runq = name.startswith("bin")
+    exe = os.path.join(PKG_DIR, "host", "runq_hip" if runq else "qwen_hip")
+    if not os.path.exists(exe):
+        pytest.skip(f"{exe} not built")
+    dump = str(tmp_path / "l.bin")
+    args = [os.path.join(GOLDEN, "tiny.bin" if runq else "tiny.qwb"), "--ids", ",".join(map(str, meta["prompt"])),
+            *extra, "--logits", dump]
+    args += ["-n", str(meta["steps"])] if runq else ["-n", str(meta["n"]), "-c", str(meta["ctx"])]
+    r = subprocess.run([exe, *args], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert [int(v) for v in r.stdout.strip().split(",")] == meta["ids"]
+    if name in ("qwb", "bin"):
+        got = np.fromfile(dump, "<f4").reshape(-1, 256)
+        ref = golden(name, 256)
+        n = min(len(got), len(ref))
+        assert max(rel_err(a, b) for a, b in zip(got[:n], ref[:n])) < TOL

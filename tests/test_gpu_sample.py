@@ -124,13 +124,17 @@ def test_device_sampler_matches_oracle(n, topp):
 
 
 def test_all_equal_logits_take_ties_in_index_order():
-    """top-p over n equal probabilities: every row is a candidate, the sort keeps index order (as the
-    reference's qsort over its index-ordered candidates does for equal keys), so the draw is row
-    floor(coin * cumulative / p) of the prefix"""
+    """top-p over n equal probabilities: every row is a candidate and equal probabilities keep row order (as
+    the reference's qsort over its row-ordered candidates does for equal keys), so the draw is the row
+    floor(coin * cumulative / p) of the prefix.  The reference's fp32 running sum of 0.001 drifts by a
+    fraction of a row over 500 terms, so its row can be one off; the device's is the exact one."""
     lg = np.zeros((32, 1000), np.float32)
-    got, _ = pkg().sample(lg, 1.0, 0.5, 99)
-    want, _, _ = oracle_rows(lg, 1.0, 0.5, 99)
-    assert np.array_equal(got, want)
+    got, st_g = pkg().sample(lg, 1.0, 0.5, 99)
+    want, st_o, draws = oracle_rows(lg, 1.0, 0.5, 99)
+    assert st_g == st_o
+    assert np.abs(got - want).max() <= 1
+    for row, (p, coin) in zip(got, draws):
+        assert exact_choice(p, coin, 0.5, int(row))
     assert got.max() <= 501  # the prefix passes topp = 0.5 after ~500 equal candidates
 
 
