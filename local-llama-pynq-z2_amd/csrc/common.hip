@@ -29,9 +29,19 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     GemvShape s;
     const int C = T.nchunks;
     if (cus < 1) cus = 1;
+    s.ord = 0;
     if (ordered) {
-        s.kw = 1;
-        s.nb = 4;
+        // Ordered sums (runq): the unordered split when the group products of one iteration's rows fit in
+        // 64 KiB of LDS (they are then added per row in group order), else one wave per 64-row block whose
+        // lanes each own a row and add its groups in order.
+        gemv_split(s, C, 4, T, epi);
+        if ((size_t)s.nb * T.rb * (T.ng + 1) * 4 <= 65536) {
+            s.ord = 1;
+            ordered = 0; // shaped like the unordered GEMV from here on
+        } else {
+            s.kw = 1;
+            s.nb = 4;
+        }
     } else {
         gemv_split(s, C, 4, T, epi);
     }
@@ -41,6 +51,7 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     if (iters > resident) {
         if (!ordered) {
             gemv_split(s, C, 16, T, epi);
+            if (s.ord && (size_t)s.nb * T.rb * (T.ng + 1) * 4 > 65536) s.nb = 1; // keep the products in LDS
             iters = (T.nblocks + s.nb - 1) / s.nb;
             waves = s.kw * s.nb;
             resident = cus * (waves < 16 ? 16 / waves : 1);

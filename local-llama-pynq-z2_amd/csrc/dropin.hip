@@ -130,6 +130,7 @@ int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out
     a.kw = W->shape.kw;
     a.nb = W->shape.nb;
     a.depth = W->shape.depth;
+    a.ord = W->shape.ord;
     a.xq = xdev;
     a.xs = (const float *)xs;
     a.out = (float *)out;

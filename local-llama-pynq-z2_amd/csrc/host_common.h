@@ -35,6 +35,7 @@ static inline int hip_device_from_env(const char *who) {
 // the device's compute-unit count (hip_cu_count).
 struct GemvShape {
     int kw, nb, grid, depth;
+    int ord; // ordered sums through LDS group products (GemvArgs::ord)
 };
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus);
 

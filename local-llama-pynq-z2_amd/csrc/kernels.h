@@ -41,6 +41,7 @@ struct GemvArgs {
     TiledMat W;
     int kw, nb;             // waves per row-block, row-blocks per block iteration (a power of two)
     int depth;              // weight batches in flight per wave: 2 or 4
+    int ord;                // 1: each row's group products are added in group order (bit-exact sequential sum)
     // derived by launch_gemv: log2(nb), log2(W.rb), iterations, chunks per wave (kw_base + (my_kw < kw_rem)),
     // iterations per block (it_base + (block < it_rem))
     int nb_log2, rb_log2, n_it, kw_base, kw_rem, it_base, it_rem;

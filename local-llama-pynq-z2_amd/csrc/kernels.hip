@@ -163,6 +163,27 @@ __device__ __forceinline__ void merge_weights(float2 st, int h, int k, int S, in
     if (ok) wgt[h * S + k] = f * (1.0f / l);
 }
 
+// Ordered mode: the batch's group products p_g = ((float)ival * ws) * xs, each stored at (row, group) in LDS,
+// so that one lane per row can add them in group order afterwards (runq.c:452-456 adds them sequentially).
+template <int WB, int GSZ, int SF32>
+__device__ __forceinline__ void store_batch(float *sprod, int ng, int row_l, int nchunks, int c0, int kw, int gpc,
+                                            int g_lane, const int8_t *sxq, const float *sxs,
+                                            const uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
+                                            const uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+    using F = Fmt<WB, GSZ, SF32>;
+#pragma unroll
+    for (int u = 0; u < F::UNROLL; u++) {
+        const int c = c0 + u * kw, g = c * gpc + g_lane;
+        if (c < nchunks && g < ng) { // groups past n (padding of the last chunk) have no slot
+            const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
+            const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
+            float p = (float)iv * sc; // qwen.c:452, runq.c:452
+            p = p * sxs[g];
+            sprod[row_l * (ng + 1) + g] = p;
+        }
+    }
+}
+
 // 16 bytes as a native vector: copied as a register value (a struct copy would go through memory)
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -184,7 +205,11 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     float *sxs = (float *)(lds + (size_t)ngp * GSZ);      // ngp4
     float *sred = sxs + ngp4;                             // nw * 64
     float *srow = sred + nw * WAVE;                       // nb * rb
-    float *sv = srow + a.nb * rb;                         // prologue / epilogue floats
+    // ordered mode: the group products of the iteration's rows, rows_it x (ng + 1) (padded against bank
+    // conflicts), summed per row in group order by finish()
+    const int ngs = W.ng + 1;
+    float *sprod = srow + a.nb * rb;
+    float *sv = sprod + (a.ord ? a.nb * rb * ngs : 0);    // prologue / epilogue floats
     // wave = my_kw * nb + my_nb (nb a power of two); the launcher precomputes every quotient the shape needs
     const int my_nb = wave & (a.nb - 1), my_kw = wave >> a.nb_log2;
     const int rows_it = a.nb * rb;
@@ -391,14 +416,24 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     int best_i = 0x7fffffff;
     auto finish = [&](int it, float acc) {
         KERNEL_MARK(5);
-        acc = wave_sum_from(acc, rb); // lanes holding the same row
-        if (lane < rb) sred[wave * rb + lane] = acc;
-        __syncthreads();
-        if (tid < rows_it) {
-            const int nbi = tid >> a.rb_log2, r = tid & (rb - 1);
-            float v = 0.0f;
-            for (int k = 0; k < a.kw; k++) v += sred[(k * a.nb + nbi) * rb + r];
-            srow[tid] = v;
+        if (a.ord) { // every group product is in LDS: one thread per row adds them in group order
+            __syncthreads();
+            if (tid < rows_it) {
+                const float *pr = sprod + tid * ngs;
+                float v = 0.0f;
+                for (int g = 0; g < W.ng; g++) v += pr[g];
+                srow[tid] = v;
+            }
+        } else {
+            acc = wave_sum_from(acc, rb); // lanes holding the same row
+            if (lane < rb) sred[wave * rb + lane] = acc;
+            __syncthreads();
+            if (tid < rows_it) {
+                const int nbi = tid >> a.rb_log2, r = tid & (rb - 1);
+                float v = 0.0f;
+                for (int k = 0; k < a.kw; k++) v += sred[(k * a.nb + nbi) * rb + r];
+                srow[tid] = v;
+            }
         }
         __syncthreads();
         KERNEL_MARK(6);
@@ -491,9 +526,14 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     int use_it = it0, use_bi = 0;
     float acc = 0.0f;
     auto consume = [&](const uint4 (&w)[F::UNROLL][F::PIECES], const uint32_t (&sr)[F::UNROLL]) {
-        if (use_it * a.nb + my_nb < W.nblocks)
-            acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, my_kw + use_bi * F::UNROLL * a.kw, a.kw, gpc, g_lane, sxq,
-                                          sxs, w, sr);
+        if (use_it * a.nb + my_nb < W.nblocks) {
+            if (a.ord)
+                store_batch<WB, GSZ, SF32>(sprod, W.ng, my_nb * rb + (lane & (rb - 1)), W.nchunks,
+                                           my_kw + use_bi * F::UNROLL * a.kw, a.kw, gpc, g_lane, sxq, sxs, w, sr);
+            else
+                acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, my_kw + use_bi * F::UNROLL * a.kw, a.kw, gpc, g_lane,
+                                              sxq, sxs, w, sr);
+        }
         if (++use_bi == bpi) {
             finish(use_it, acc);
             acc = 0.0f;
@@ -535,6 +575,7 @@ size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
     const TiledMat &W = a.W;
     const int ngp = W.nchunks * (WAVE / W.rb), ngp4 = (ngp + 3) & ~3;
     size_t b = (size_t)ngp * W.gs + (size_t)ngp4 * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
+    if (a.ord) b += (size_t)a.nb * W.rb * (W.ng + 1) * 4; // group products of the ordered mode
     size_t extra = 0;
     if (pro == PRO_NORM) extra = (size_t)W.n * 8;
     if (pro == PRO_ATTN) extra = (size_t)W.n * 4 + (size_t)a.n_heads * a.att_splits * 4;

@@ -112,6 +112,7 @@ GemvArgs base_args(const llm_model *m, const TiledMat &T, const GemvShape &s) {
     a.kw = s.kw;
     a.nb = s.nb;
     a.depth = s.depth;
+    a.ord = s.ord;
     a.qflavor = m->qflavor;
     a.ctrl = m->ctrl;
     a.eps = m->info.rms_eps;
