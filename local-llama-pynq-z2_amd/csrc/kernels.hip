@@ -312,6 +312,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
 
     KERNEL_MARK(1);
     // (4) prologue: int8 activations and their scales into LDS
+    bool in_regs = false; // PRO_NORM: normalized and quantized straight from the registers
     if constexpr (PRO == PRO_XQ) {
         const int nq = n / 16;
         u32x4 *dst = (u32x4 *)sxq;
@@ -353,15 +354,27 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
             ss /= (float)n;
             ss += a.eps;
             ss = 1.0f / sqrtf(ss);
+            in_regs = nv <= PRO_VEC * nt;
+            if (in_regs) { // the whole vector is in registers: normalize and quantize in one pass
 #pragma unroll
-            for (int k = 0; k < PRO_VEC; k++)
-                if (tid + k * nt < nv) {
-                    const float4 v = pn[k], g = pg[k];
-                    sv4[tid + k * nt] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
+                for (int k = 0; k < PRO_VEC; k++)
+                    if (k * nt < nv) { // uniform; a slot past nv belongs to a group that is wholly past it
+                        const int i = tid + k * nt;
+                        const float4 v = pn[k], g = pg[k];
+                        const float4 o = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
+                        quantize_slot(o, i, i < nv, W.gs, a.qflavor, sxq, sxs);
+                    }
+            } else {
+#pragma unroll
+                for (int k = 0; k < PRO_VEC; k++)
+                    if (tid + k * nt < nv) {
+                        const float4 v = pn[k], g = pg[k];
+                        sv4[tid + k * nt] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
+                    }
+                for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
+                    const float4 v = sv4[i], g = sv4[nv + i];
+                    sv4[i] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
                 }
-            for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
-                const float4 v = sv4[i], g = sv4[nv + i];
-                sv4[i] = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
             }
         } else { // PRO_ATTN: merge the attention slices of every head, then xb = acc / l
             // statistics: SW lanes per head, lane k holds slice k
@@ -400,9 +413,11 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                 if (v0 + tid < nv) sv4[v0 + tid] = acc;
             }
         }
-        __syncthreads();
-        KERNEL_MARK(3);
-        block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
+        if (!in_regs) {
+            __syncthreads();
+            KERNEL_MARK(3);
+            block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
+        }
         for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
     }
     for (int i = W.ng + tid; i < ngp; i += nt) sxs[i] = 0.0f;
