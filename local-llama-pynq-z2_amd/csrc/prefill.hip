@@ -41,23 +41,18 @@ __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
     const int rb = W.rb, gpc = WAVE / rb, n = W.n, ng = W.ng;
     const int rowA = min(r0 + rl, W.rows - 1), tok = min(m0 + rl, a.M - 1);
     const int bA = rowA / rb, laneA = rowA - bA * rb; // + gi * rb per group
-    // scale rows r0 + 8i + 4h .. +3: four rows of one row-block, contiguous in the record's scale area
-    int bS[4], laneS[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int R4 = min(r0 + 8 * i + 4 * h, W.rows - 4);
-        bS[i] = R4 / rb;
-        laneS[i] = R4 - bS[i] * rb;
-    }
+    // Each lane loads and converts the scale of its A row (rows r0 .. r0 + 31 over lanes 0..31) and shares it
+    // through LDS; a lane's 16 outputs need rows r0 + 8i + 4h .. +3 (i = 0..3).
+    __shared__ __align__(16) float s_sc[32];
     const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
     const float *xsrow = a.xs + (size_t)tok * ng;
 
     // A ring of PF_STAGES groups in flight.  A stage holds raw loaded words only: the int4 unpacking and the
     // scale conversion happen when the group is used, so issuing a stage never waits for its loads.
-    constexpr int NS = PF_STAGES, SCW = SF32 ? 4 : 2; // SCW: 32-bit words of one row quad's scales
+    constexpr int NS = PF_STAGES;
     uint4 wr[NS][KC];                                 // int4: the lane's 16-byte segment; int8: the K-half piece
     v4i bv[NS][KC];
-    uint32_t sr[NS][4][SCW];
+    uint32_t sr[NS];                                  // raw scale of the lane's A row
     float xs[NS];
     auto load = [&](int g, int st) {
         const int c = g / gpc, gi = g - c * gpc;
@@ -68,21 +63,9 @@ __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
             else wr[st][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
             bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint8_t *sp = W.data + ((size_t)bS[i] * W.nchunks + c) * W.rec + 64 * SB + (size_t)(gi * rb + laneS[i]) * SCB;
-            if constexpr (SF32) {
-                const uint4 u = *(const uint4 *)sp;
-                sr[st][i][0] = u.x;
-                sr[st][i][1] = u.y;
-                sr[st][i][2] = u.z;
-                sr[st][i][3] = u.w;
-            } else {
-                const uint2 u = *(const uint2 *)sp;
-                sr[st][i][0] = u.x;
-                sr[st][i][1] = u.y;
-            }
-        }
+        const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA) * SCB;
+        if constexpr (SF32) sr[st] = *(const uint32_t *)sp;
+        else sr[st] = *(const uint16_t *)sp;
         xs[st] = xsrow[g];
     };
     float acc[16];
@@ -103,13 +86,20 @@ __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
             }
             d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d, 0, 0, 0);
         }
+        // the group's row scales: one conversion per lane, shared through LDS (the block is this one wave, so
+        // the barriers cost next to nothing)
+        const float mine = SF32 ? __uint_as_float(sr[st]) : f16_bits_to_f32((uint16_t)sr[st]) * (WB == 4 ? 0.0625f : 1.0f);
+        if (h == 0) s_sc[rl] = mine;
+        __syncthreads();
+        float4 ws4[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) ws4[i] = *(const float4 *)(s_sc + 8 * i + 4 * h);
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                float ws;
-                if constexpr (SF32) ws = __uint_as_float(sr[st][i][j]);
-                else ws = f16_bits_to_f32((uint16_t)(sr[st][i][j >> 1] >> (16 * (j & 1)))) * (WB == 4 ? 0.0625f : 1.0f);
+                const float ws = j == 0 ? ws4[i].x : j == 1 ? ws4[i].y : j == 2 ? ws4[i].z : ws4[i].w;
                 float p = (float)d[4 * i + j] * ws; // qwen.c:452, runq.c:452
                 p = p * xs[st];
                 acc[4 * i + j] = acc[4 * i + j] + p;
