@@ -18,92 +18,116 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 // ------------------------------------------------------------------------------------------------------
 // GEMM: y[m][r] = sum_g ((float)ival(r, m, g) * ws[r][g]) * xs[m][g], groups in order.
 //
-// One wave per 32 rows x 32 tokens.  v_mfma_i32_32x32x32_i8 lane layout: A (rows x K): lane l holds row l%32,
-// K = 16 (l/32) .. +16; B (K x tokens): token l%32, same K half; D: token l%32, rows 8i + 4 (l/32) + j in
-// d[4i + j].  int4 weights enter as 16 * q (the nibble at the top of its byte, as in the GEMV), so D holds
-// 16 * ival; their fp16 scales are taken as ws / 16, an exact power-of-two step, and (16 ival) * (ws / 16)
-// rounds to the same float as ival * ws.
+// One wave per PF_RT x 32 rows x 32 tokens (PF_RT MFMAs per group share the token operand).  Lane layout
+// of one MFMA: A (rows x K): lane l holds row l%32, K = 16 (l/32) .. +16; B (K x tokens): token l%32, same K
+// half; D: token l%32, rows 8i + 4 (l/32) + j in d[4i + j].  int4 weights enter as 16 * q (the nibble at the
+// top of its byte, as in the GEMV), so D holds 16 * ival; their fp16 scales are taken as ws / 16, an exact
+// power-of-two step, and (16 ival) * (ws / 16) rounds to the same float as ival * ws.
 //
 // Blocks are laid out so that all token tiles of one row tile run on the same XCD (block b goes to XCD b % 8):
 // each weight tile is read from HBM once and served from that XCD's L2 to its other token tiles.
+#define PF_RT 1 // 32-row tiles per wave (2 measured slower: the extra registers halve the waves per SIMD)
 
 template <int WB, int GSZ, int SF32>
 __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
-    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32;
+    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32, RT = PF_RT;
     const TiledMat &W = a.W;
-    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
+    const int xt = (W.rows + 32 * RT - 1) / (32 * RT), yt = (a.M + 31) / 32;
     // block -> (row tile, token tile): XCD j = b % 8 takes row tiles j, j + 8, ...
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
     const int tx = xcd + 8 * (idx / yt), ty = idx - (idx / yt) * yt;
     if (tx >= xt) return;
     const int l = threadIdx.x, h = l >> 5, rl = l & 31;
-    const int r0 = tx * 32, m0 = ty * 32;
+    const int r0 = tx * 32 * RT, m0 = ty * 32;
     const int rb = W.rb, gpc = WAVE / rb, n = W.n, ng = W.ng;
-    const int rowA = min(r0 + rl, W.rows - 1), tok = min(m0 + rl, a.M - 1);
-    const int bA = rowA / rb, laneA = rowA - bA * rb; // + gi * rb per group
-    // Each lane loads and converts the scale of its A row (rows r0 .. r0 + 31 over lanes 0..31) and shares it
-    // through LDS; a lane's 16 outputs need rows r0 + 8i + 4h .. +3 (i = 0..3).
-    __shared__ __align__(16) float s_sc[32];
+    const int tok = min(m0 + rl, a.M - 1);
+    int bA[RT], laneA[RT]; // the lane's A row of each row tile: record block and lane (+ gi * rb per group)
+#pragma unroll
+    for (int t = 0; t < RT; t++) {
+        const int rowA = min(r0 + 32 * t + rl, W.rows - 1);
+        bA[t] = rowA / rb;
+        laneA[t] = rowA - bA[t] * rb;
+    }
+    // Each lane loads and converts the scale of its A rows and shares them through LDS; a lane's outputs
+    // need rows r0 + 32t + 8i + 4h .. +3 (t < RT, i = 0..3).
+    __shared__ __align__(16) float s_sc[32 * RT];
     const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
     const float *xsrow = a.xs + (size_t)tok * ng;
 
     // A ring of PF_STAGES groups in flight.  A stage holds raw loaded words only: the int4 unpacking and the
     // scale conversion happen when the group is used, so issuing a stage never waits for its loads.
     constexpr int NS = PF_STAGES;
-    uint4 wr[NS][KC];                                 // int4: the lane's 16-byte segment; int8: the K-half piece
+    uint4 wr[NS][RT][KC];                             // int4: the lane's 16-byte segment; int8: the K-half piece
     v4i bv[NS][KC];
-    uint32_t sr[NS];                                  // raw scale of the lane's A row
+    uint32_t sr[NS][RT];                              // raw scales of the lane's A rows
     float xs[NS];
     auto load = [&](int g, int st) {
         const int c = g / gpc, gi = g - c * gpc;
-        const uint8_t *recA = W.data + ((size_t)bA * W.nchunks + c) * W.rec;
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) {
-            if constexpr (WB == 4) wr[st][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
-            else wr[st][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
-            bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
+        for (int t = 0; t < RT; t++) {
+            const uint8_t *recA = W.data + ((size_t)bA[t] * W.nchunks + c) * W.rec;
+#pragma unroll
+            for (int kc = 0; kc < KC; kc++) {
+                if constexpr (WB == 4) wr[st][t][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA[t]) * 16);
+                else wr[st][t][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA[t]) * 16);
+            }
+            const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA[t]) * SCB;
+            if constexpr (SF32) sr[st][t] = *(const uint32_t *)sp;
+            else sr[st][t] = *(const uint16_t *)sp;
         }
-        const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA) * SCB;
-        if constexpr (SF32) sr[st] = *(const uint32_t *)sp;
-        else sr[st] = *(const uint16_t *)sp;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
         xs[st] = xsrow[g];
     };
-    float acc[16];
+    float acc[RT][16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) acc[k] = 0.0f;
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc[t][k] = 0.0f;
     auto compute = [&](int st) {
-        v16i d = {};
+        v16i d[RT];
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) {
-            v4i av;
-            if constexpr (WB == 4) {
-                const uint4 w = wr[st][kc];
-                const uint32_t m = 0xF0F0F0F0u;
-                if (h == 0) av = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m), (int)((w.w << 4) & m)};
-                else av = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
-            } else {
-                av = v4i{(int)wr[st][kc].x, (int)wr[st][kc].y, (int)wr[st][kc].z, (int)wr[st][kc].w};
+        for (int t = 0; t < RT; t++) {
+            d[t] = v16i{};
+#pragma unroll
+            for (int kc = 0; kc < KC; kc++) {
+                v4i av;
+                if constexpr (WB == 4) {
+                    const uint4 w = wr[st][t][kc];
+                    const uint32_t m = 0xF0F0F0F0u;
+                    if (h == 0) av = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m), (int)((w.w << 4) & m)};
+                    else av = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
+                } else {
+                    av = v4i{(int)wr[st][t][kc].x, (int)wr[st][t][kc].y, (int)wr[st][t][kc].z, (int)wr[st][t][kc].w};
+                }
+                d[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d[t], 0, 0, 0);
             }
-            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d, 0, 0, 0);
         }
-        // the group's row scales: one conversion per lane, shared through LDS (the block is this one wave, so
-        // the barriers cost next to nothing)
-        const float mine = SF32 ? __uint_as_float(sr[st]) : f16_bits_to_f32((uint16_t)sr[st]) * (WB == 4 ? 0.0625f : 1.0f);
-        if (h == 0) s_sc[rl] = mine;
+        // the group's row scales: one conversion per lane and row tile, shared through LDS (the block is this
+        // one wave, so the barriers cost next to nothing)
+        if (h == 0)
+#pragma unroll
+            for (int t = 0; t < RT; t++)
+                s_sc[32 * t + rl] = SF32 ? __uint_as_float(sr[st][t])
+                                         : f16_bits_to_f32((uint16_t)sr[st][t]) * (WB == 4 ? 0.0625f : 1.0f);
         __syncthreads();
-        float4 ws4[4];
+        float4 ws4[RT][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) ws4[i] = *(const float4 *)(s_sc + 8 * i + 4 * h);
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ws4[t][i] = *(const float4 *)(s_sc + 32 * t + 8 * i + 4 * h);
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int t = 0; t < RT; t++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float ws = j == 0 ? ws4[i].x : j == 1 ? ws4[i].y : j == 2 ? ws4[i].z : ws4[i].w;
-                float p = (float)d[4 * i + j] * ws; // qwen.c:452, runq.c:452
-                p = p * xs[st];
-                acc[4 * i + j] = acc[4 * i + j] + p;
-            }
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float ws = j == 0 ? ws4[t][i].x : j == 1 ? ws4[t][i].y : j == 2 ? ws4[t][i].z : ws4[t][i].w;
+                    float p = (float)d[t][4 * i + j] * ws; // qwen.c:452, runq.c:452
+                    p = p * xs[st];
+                    acc[t][4 * i + j] = acc[t][4 * i + j] + p;
+                }
     };
 #pragma unroll
     for (int st = 0; st < NS - 1; st++)
@@ -120,14 +144,16 @@ __global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
     const int m = m0 + rl;
     if (m < a.M) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int R = r0 + 8 * i + 4 * h;
-            float *dst = a.y + (size_t)m * W.rows + R;
-            if (R + 3 < W.rows) *(float4 *)dst = make_float4(acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]);
-            else
-                for (int j = 0; j < 4; j++)
-                    if (R + j < W.rows) dst[j] = acc[4 * i + j];
-        }
+        for (int t = 0; t < RT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int R = r0 + 32 * t + 8 * i + 4 * h;
+                float *dst = a.y + (size_t)m * W.rows + R;
+                if (R + 3 < W.rows) *(float4 *)dst = make_float4(acc[t][4 * i], acc[t][4 * i + 1], acc[t][4 * i + 2], acc[t][4 * i + 3]);
+                else
+                    for (int j = 0; j < 4; j++)
+                        if (R + j < W.rows) dst[j] = acc[t][4 * i + j];
+            }
     }
 }
 
@@ -137,7 +163,7 @@ hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStre
     if (a.M < 1 || W.rows % 4 || W.n % gs || W.n % 16 || ((uintptr_t)a.xq & 15) || ((uintptr_t)a.y & 15) ||
         W.gs != gs || W.wbits != wbits || W.sf32 != sf32)
         return hipErrorInvalidValue;
-    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
+    const int xt = (W.rows + 32 * PF_RT - 1) / (32 * PF_RT), yt = (a.M + 31) / 32;
     const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * yt);
 #define PG(WB_, GS_, SF_)                                                                                      \
     if (wbits == WB_ && gs == GS_ && sf32 == SF_) {                                                           \
