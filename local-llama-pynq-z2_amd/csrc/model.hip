@@ -565,10 +565,13 @@ int load_qwb(llm_model *m, const char *path, int ctx) {
     total += round256(m->head.bytes);
     I.weight_bytes = (double)total;
     if (dalloc(m, &m->wts, total)) return -1;
-    // staging for the largest raw group (the head, or a layer's fused matrices)
-    size_t stage_b = round256((size_t)I.n_logits * dim) + round256((size_t)I.n_logits * dim / 16) + 4096;
-    const size_t gu_raw = 2 * (round256((size_t)hid * dim / 2) + round256((size_t)hid * dim / 16));
-    if (gu_raw + 4096 > stage_b) stage_b = gu_raw + 4096;
+    // staging for the largest raw group (the head, or a layer's fused matrices): each plane rounded to 256 B
+    auto q4_raw = [](size_t rows, size_t n) { return round256(rows * n / 2) + round256(rows * n / 16); };
+    size_t stage_b = round256((size_t)I.n_logits * dim) + round256((size_t)I.n_logits * dim / 16);
+    stage_b = std::max(stage_b, q4_raw(dim, dim) + 2 * q4_raw(kv, dim)); // qkv
+    stage_b = std::max(stage_b, 2 * q4_raw(hid, dim));                   // gate, up
+    stage_b = std::max(stage_b, q4_raw(dim, hid));                       // down (o: dim x dim, within qkv)
+    stage_b += 4096;
     uint8_t *stage;
     int *rowmap_d;
     const int max_rows = I.n_logits > 2 * hid ? I.n_logits : 2 * hid;

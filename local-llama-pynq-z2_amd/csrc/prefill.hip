@@ -6,154 +6,160 @@
 // GEMV reads, with the per-group int32 sums exact and the group terms p = ((float)ival * ws) * xs added in
 // group order, which is the reference's matmul (qwen.c:436-456, runq.c:429-458) for every (row, token).
 // The element-wise steps of forward() run per token, and attention is causal over the KV cache.
+#include <type_traits>
+
 #include "attn.h"
 #include "prefill.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// groups of the prefill GEMM's K loop whose loads are in flight at once
+// K groups of each wave of the prefill GEMM whose loads are in flight at once (one per chunk)
+#ifndef PF_STAGES
 #define PF_STAGES 4
+#endif
 
 // ------------------------------------------------------------------------------------------------------
 // GEMM: y[m][r] = sum_g ((float)ival(r, m, g) * ws[r][g]) * xs[m][g], groups in order.
 //
-// One wave per PF_RT x 32 rows x 32 tokens (PF_RT MFMAs per group share the token operand).  Lane layout
-// of one MFMA: A (rows x K): lane l holds row l%32, K = 16 (l/32) .. +16; B (K x tokens): token l%32, same K
-// half; D: token l%32, rows 8i + 4 (l/32) + j in d[4i + j].  int4 weights enter as 16 * q (the nibble at the
-// top of its byte, as in the GEMV), so D holds 16 * ival; their fp16 scales are taken as ws / 16, an exact
-// power-of-two step, and (16 ival) * (ws / 16) rounds to the same float as ival * ws.
+// One block of PF_KW = 4 waves per 32 rows x 32 tokens.  The K groups are dealt round-robin over the waves:
+// in chunk c wave w takes group 4c + w, runs its MFMA and forms the group's 16 products per lane; the
+// products go through LDS and each thread adds, for its 4 outputs, the chunk's 4 products in group order.
+// The sum is therefore the sequential one, while the MFMA, unpacking and product work is spread over the
+// four SIMDs of a CU (a single wave per tile leaves the down projection's 152 groups on one SIMD).
+//
+// Lane layout of one MFMA: A (rows x K): lane l holds row l%32, K = 16 (l/32) .. +16; B (K x tokens): token
+// l%32, same K half; D: token l%32, rows 8i + 4 (l/32) + j in d[4i + j].  int4 weights enter as 16 * q (the
+// nibble at the top of its byte, as in the GEMV), so D holds 16 * ival; their fp16 scales are taken as
+// ws / 16, an exact power-of-two step, and (16 ival) * (ws / 16) rounds to the same float as ival * ws.
+// Thread (w, l) owns the outputs of slot i = w: token l%32, rows 8w + 4 (l/32) .. +3.
 //
 // Blocks are laid out so that all token tiles of one row tile run on the same XCD (block b goes to XCD b % 8):
 // each weight tile is read from HBM once and served from that XCD's L2 to its other token tiles.
-#define PF_RT 1 // 32-row tiles per wave (2 measured slower: the extra registers halve the waves per SIMD)
+#define PF_KW 4
 
 template <int WB, int GSZ, int SF32>
-__global__ void __launch_bounds__(64) k_pgemm(PgemmArgs a) {
-    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32, RT = PF_RT;
+__global__ void __launch_bounds__(64 * PF_KW) k_pgemm(PgemmArgs a) {
+    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32, KW = PF_KW;
     const TiledMat &W = a.W;
-    const int xt = (W.rows + 32 * RT - 1) / (32 * RT), yt = (a.M + 31) / 32;
+    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
     // block -> (row tile, token tile): XCD j = b % 8 takes row tiles j, j + 8, ...
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
     const int tx = xcd + 8 * (idx / yt), ty = idx - (idx / yt) * yt;
-    if (tx >= xt) return;
-    const int l = threadIdx.x, h = l >> 5, rl = l & 31;
-    const int r0 = tx * 32 * RT, m0 = ty * 32;
+    if (tx >= xt) return; // the whole block
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, h = l >> 5, rl = l & 31;
+    const int r0 = tx * 32, m0 = ty * 32;
     const int rb = W.rb, gpc = WAVE / rb, n = W.n, ng = W.ng;
     const int tok = min(m0 + rl, a.M - 1);
-    int bA[RT], laneA[RT]; // the lane's A row of each row tile: record block and lane (+ gi * rb per group)
-#pragma unroll
-    for (int t = 0; t < RT; t++) {
-        const int rowA = min(r0 + 32 * t + rl, W.rows - 1);
-        bA[t] = rowA / rb;
-        laneA[t] = rowA - bA[t] * rb;
-    }
-    // Each lane loads and converts the scale of its A rows and shares them through LDS; a lane's outputs
-    // need rows r0 + 32t + 8i + 4h .. +3 (t < RT, i = 0..3).
-    __shared__ __align__(16) float s_sc[32 * RT];
+    const int rowA = min(r0 + rl, W.rows - 1), bA = rowA / rb, laneA = rowA - bA * rb;
+    // per wave: the converted scales of the tile's 32 rows for its current group (lanes rl convert row rl,
+    // every lane reads rows 8i + 4h .. +3); per chunk (two buffers): every wave's products, [wave][i][lane]
+    __shared__ __align__(16) float s_sc[KW][32];
+    __shared__ __align__(16) float4 s_p[2][KW][4][WAVE];
     const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
     const float *xsrow = a.xs + (size_t)tok * ng;
 
-    // A ring of PF_STAGES groups in flight.  A stage holds raw loaded words only: the int4 unpacking and the
-    // scale conversion happen when the group is used, so issuing a stage never waits for its loads.
+    // A ring of PF_STAGES of this wave's groups in flight.  A stage holds raw loaded words only: the int4
+    // unpacking and the scale conversion happen when the group is used, so issuing a stage never waits.
     constexpr int NS = PF_STAGES;
-    uint4 wr[NS][RT][KC];                             // int4: the lane's 16-byte segment; int8: the K-half piece
+    uint4 wr[NS][KC]; // int4: the lane's 16-byte segment; int8: the K-half piece
     v4i bv[NS][KC];
-    uint32_t sr[NS][RT];                              // raw scales of the lane's A rows
+    using ScaleBits = typename std::conditional<SF32 != 0, uint32_t, uint16_t>::type;
+    ScaleBits sr[NS]; // raw scale of the lane's A row
     float xs[NS];
     auto load = [&](int g, int st) {
         const int c = g / gpc, gi = g - c * gpc;
+        const uint8_t *recA = W.data + ((size_t)bA * W.nchunks + c) * W.rec;
 #pragma unroll
-        for (int t = 0; t < RT; t++) {
-            const uint8_t *recA = W.data + ((size_t)bA[t] * W.nchunks + c) * W.rec;
-#pragma unroll
-            for (int kc = 0; kc < KC; kc++) {
-                if constexpr (WB == 4) wr[st][t][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA[t]) * 16);
-                else wr[st][t][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA[t]) * 16);
-            }
-            const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA[t]) * SCB;
-            if constexpr (SF32) sr[st][t] = *(const uint32_t *)sp;
-            else sr[st][t] = *(const uint16_t *)sp;
+        for (int kc = 0; kc < KC; kc++) {
+            if constexpr (WB == 4) wr[st][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
+            else wr[st][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
         }
+        const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA) * SCB;
+        sr[st] = *(const ScaleBits *)sp;
 #pragma unroll
         for (int kc = 0; kc < KC; kc++) bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
         xs[st] = xsrow[g];
     };
-    float acc[RT][16];
+    // the products of stage st into s_p[buf][w]
+    auto products = [&](int st, int buf) {
+        v16i d = v16i{};
 #pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int k = 0; k < 16; k++) acc[t][k] = 0.0f;
-    auto compute = [&](int st) {
-        v16i d[RT];
-#pragma unroll
-        for (int t = 0; t < RT; t++) {
-            d[t] = v16i{};
-#pragma unroll
-            for (int kc = 0; kc < KC; kc++) {
-                v4i av;
-                if constexpr (WB == 4) {
-                    const uint4 w = wr[st][t][kc];
-                    const uint32_t m = 0xF0F0F0F0u;
-                    if (h == 0) av = v4i{(int)((w.x << 4) & m), (int)((w.y << 4) & m), (int)((w.z << 4) & m), (int)((w.w << 4) & m)};
-                    else av = v4i{(int)(w.x & m), (int)(w.y & m), (int)(w.z & m), (int)(w.w & m)};
-                } else {
-                    av = v4i{(int)wr[st][t][kc].x, (int)wr[st][t][kc].y, (int)wr[st][t][kc].z, (int)wr[st][t][kc].w};
-                }
-                d[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d[t], 0, 0, 0);
+        for (int kc = 0; kc < KC; kc++) {
+            v4i av;
+            if constexpr (WB == 4) {
+                const uint4 q = wr[st][kc];
+                const uint32_t m = 0xF0F0F0F0u;
+                if (h == 0) av = v4i{(int)((q.x << 4) & m), (int)((q.y << 4) & m), (int)((q.z << 4) & m), (int)((q.w << 4) & m)};
+                else av = v4i{(int)(q.x & m), (int)(q.y & m), (int)(q.z & m), (int)(q.w & m)};
+            } else {
+                av = v4i{(int)wr[st][kc].x, (int)wr[st][kc].y, (int)wr[st][kc].z, (int)wr[st][kc].w};
             }
+            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d, 0, 0, 0);
         }
-        // the group's row scales: one conversion per lane and row tile, shared through LDS (the block is this
-        // one wave, so the barriers cost next to nothing)
+        // one scale conversion per lane, exchanged within the wave through its own LDS slots
         if (h == 0)
+            s_sc[w][rl] = SF32 ? __uint_as_float(sr[st]) : f16_bits_to_f32(sr[st]) * (WB == 4 ? 0.0625f : 1.0f);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int t = 0; t < RT; t++)
-                s_sc[32 * t + rl] = SF32 ? __uint_as_float(sr[st][t])
-                                         : f16_bits_to_f32((uint16_t)sr[st][t]) * (WB == 4 ? 0.0625f : 1.0f);
-        __syncthreads();
-        float4 ws4[RT][4];
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) ws4[t][i] = *(const float4 *)(s_sc + 32 * t + 8 * i + 4 * h);
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float ws = j == 0 ? ws4[t][i].x : j == 1 ? ws4[t][i].y : j == 2 ? ws4[t][i].z : ws4[t][i].w;
-                    float p = (float)d[t][4 * i + j] * ws; // qwen.c:452, runq.c:452
-                    p = p * xs[st];
-                    acc[t][4 * i + j] = acc[t][4 * i + j] + p;
-                }
+        for (int i = 0; i < 4; i++) {
+            const float4 ws4 = *(const float4 *)(&s_sc[w][8 * i + 4 * h]);
+            float4 p;
+            p.x = (float)d[4 * i] * ws4.x; // qwen.c:452, runq.c:452
+            p.y = (float)d[4 * i + 1] * ws4.y;
+            p.z = (float)d[4 * i + 2] * ws4.z;
+            p.w = (float)d[4 * i + 3] * ws4.w;
+            p.x = p.x * xs[st];
+            p.y = p.y * xs[st];
+            p.z = p.z * xs[st];
+            p.w = p.w * xs[st];
+            s_p[buf][w][i][l] = p;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier(); // this wave's scale reads come before its next group's scale writes
     };
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int nc = (ng + KW - 1) / KW; // chunks; wave w's group in chunk c is KW c + w when below ng
+    // Every stage is loaded and used, past the last group too (clamped to it; its products are not added):
+    // with no branch around the loads the compiler's count of loads in flight stays exact, so waiting for
+    // one stage does not wait for the stages issued after it.
 #pragma unroll
-    for (int st = 0; st < NS - 1; st++)
-        if (st < ng) load(st, st);
-    for (int g0 = 0; g0 < ng; g0 += NS) {
+    for (int st = 0; st < NS - 1; st++) load(min(KW * st + w, ng - 1), st);
+    for (int c0 = 0; c0 < nc; c0 += NS) {
 #pragma unroll
         for (int st = 0; st < NS; st++) {
-            const int g = g0 + st;
-            if (g >= ng) break;
-            if (g + NS - 1 < ng) load(g + NS - 1, (st + NS - 1) % NS);
-            compute(st);
+            const int c = c0 + st;
+            if (c >= nc) break;
+            load(min(KW * (c + NS - 1) + w, ng - 1), (st + NS - 1) % NS);
+            const int buf = c & 1;
+            products(st, buf); // past the last group: a clamped copy that the sum below skips
+            __syncthreads();
+            const int cnt = ng - KW * c;
+#pragma unroll
+            for (int v = 0; v < KW; v++) { // the chunk's groups in order
+                if (v < cnt) {
+                    const float4 p = s_p[buf][v][w][l];
+                    acc.x = acc.x + p.x;
+                    acc.y = acc.y + p.y;
+                    acc.z = acc.z + p.z;
+                    acc.w = acc.w + p.w;
+                }
+            }
+            // no second barrier: the next chunk writes the other buffer, and the one after that writes this
+            // buffer only after the next chunk's barrier, which every thread reaches after these reads
         }
     }
-    const int m = m0 + rl;
+    const int m = m0 + rl, R = r0 + 8 * w + 4 * h;
     if (m < a.M) {
-#pragma unroll
-        for (int t = 0; t < RT; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int R = r0 + 32 * t + 8 * i + 4 * h;
-                float *dst = a.y + (size_t)m * W.rows + R;
-                if (R + 3 < W.rows) *(float4 *)dst = make_float4(acc[t][4 * i], acc[t][4 * i + 1], acc[t][4 * i + 2], acc[t][4 * i + 3]);
-                else
-                    for (int j = 0; j < 4; j++)
-                        if (R + j < W.rows) dst[j] = acc[t][4 * i + j];
-            }
+        float *dst = a.y + (size_t)m * W.rows + R;
+        if (R + 3 < W.rows) *(float4 *)dst = acc;
+        else {
+            const float v[4] = {acc.x, acc.y, acc.z, acc.w};
+            for (int j = 0; j < 4; j++)
+                if (R + j < W.rows) dst[j] = v[j];
+        }
     }
 }
 
@@ -163,11 +169,11 @@ hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStre
     if (a.M < 1 || W.rows % 4 || W.n % gs || W.n % 16 || ((uintptr_t)a.xq & 15) || ((uintptr_t)a.y & 15) ||
         W.gs != gs || W.wbits != wbits || W.sf32 != sf32)
         return hipErrorInvalidValue;
-    const int xt = (W.rows + 32 * PF_RT - 1) / (32 * PF_RT), yt = (a.M + 31) / 32;
+    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
     const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * yt);
 #define PG(WB_, GS_, SF_)                                                                                      \
     if (wbits == WB_ && gs == GS_ && sf32 == SF_) {                                                           \
-        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_>), dim3(blocks), dim3(64), 0, st, a);                       \
+        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_>), dim3(blocks), dim3(64 * PF_KW), 0, st, a);                \
         return hipGetLastError();                                                                             \
     }
     PG(4, 32, 0)
@@ -286,8 +292,153 @@ __global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
     block_quantize(sv, hid, a.gs, a.qflavor, a.oq + (size_t)m * hid, a.os + (size_t)m * (hid / a.gs));
 }
 
+// ------------------------------------------------------------------------------------------------------
+// causal attention (qwen.c:526-546, runq.c:530-568) of the chunk's tokens over the KV cache
+//
+// The positions 0 .. p0 + m of token m are cut into slices of att_sl (a multiple of 16); each slice leaves
+// its running max, sum of exponentials and exp-weighted value sums, and k_p_attn_merge combines a token's
+// slices.  A token with a single slice gets its output straight from the slice kernel.
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+// key positions staged in LDS per step: 4 tiles of 16 (2 for a head size of 128, within 64 KB of LDS)
+__host__ __device__ constexpr int pa_kc(int hs) { return hs >= 128 ? 32 : 64; }
+
+// Block = (kv head, tile of 16 consecutive tokens, slice); wave j is query head kv_mul * kvh + j, so the K/V
+// rows staged for the slice serve all heads of the group.  fp32 MFMA (16x16x4) with lane l = 16 g + r:
+//   scores S^T = K Q^T: A lane = K[key r][dim], B lane = Q[token r][dim]; in step u lane group g takes
+//     dim g * HS/4 + u (a permutation of the dot's terms), so each lane reads its K row as 16-byte vectors;
+//     D lane = S[token r][keys 4g + i], i = 0..3: every lane's scores belong to its own token r;
+//   values O^T += V^T P^T: A lane = V[key 4g + u][16 dt + r], B lane = P[token r][key 4g + u], the lane's
+//     own probability; D lane = O[token r][16 dt + 4g + i].
+// The online softmax (running max and sum per token) therefore needs no data movement except the max over
+// the four lanes of a token.
+template <int HS>
+__global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, float *out) {
+    constexpr int H4 = HS / 4, KS = HS + 4, DT = HS / 16, PA_KC = pa_kc(HS);
+    extern __shared__ __align__(16) float sm[];
+    float *sk = sm, *sv = sm + PA_KC * KS; // [PA_KC][KS] each
+    const int kvh = blockIdx.x, m0 = 16 * blockIdx.y, s = blockIdx.z, kv_mul = a.n_heads / a.n_kv;
+    const int t_begin = s * a.att_sl;
+    const int t_stop = min(t_begin + a.att_sl, a.p0 + min(m0 + 16, a.M)); // keys of the slice any token sees
+    if (t_begin >= t_stop) return; // the whole block
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 4, r = l & 15;
+    const int h = kvh * kv_mul + w, m = min(m0 + r, a.M - 1), qlim = a.p0 + m;
+    const float rinv = 1.0f / sqrtf((float)HS);
+
+    float qv[H4];
+    {
+        const f32x4v *qp = (const f32x4v *)(a.q + (size_t)m * a.dim + (size_t)h * HS + g * H4);
+#pragma unroll
+        for (int i = 0; i < H4 / 4; i++) {
+            const f32x4v v = qp[i];
+            qv[4 * i] = v.x;
+            qv[4 * i + 1] = v.y;
+            qv[4 * i + 2] = v.z;
+            qv[4 * i + 3] = v.w;
+        }
+    }
+    f32x4v o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f; // l_run: this lane's share (its keys 4g + i) of the token's sum
+
+    for (int tc = t_begin; tc < t_stop; tc += PA_KC) {
+        const int nk = min(PA_KC, t_stop - tc);
+        // stage K and V rows tc .. tc + PA_KC - 1 (rows past the slice's last are clamped to it: finite values
+        // that the mask or a zero probability removes)
+        for (int i = tid; i < PA_KC * H4; i += nt) {
+            const int k = i / H4, c = i - k * H4;
+            const size_t gi = (size_t)(tc + min(k, nk - 1)) * a.kv_dim + (size_t)kvh * HS + 4 * c;
+            const f32x4v kk = *(const f32x4v *)(a.kc + gi), vv = *(const f32x4v *)(a.vc + gi);
+            *(f32x4v *)(sk + k * KS + 4 * c) = kk;
+            *(f32x4v *)(sv + k * KS + 4 * c) = vv;
+        }
+        __syncthreads();
+        const int ntile = (nk + 15) / 16;
+        f32x4v sc[PA_KC / 16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < PA_KC / 16; kt++) {
+            sc[kt] = f32x4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            if (kt < ntile) {
+                f32x4v d = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+                const float *kr = sk + (16 * kt + r) * KS + g * H4;
+#pragma unroll
+                for (int i = 0; i < H4 / 4; i++) {
+                    const f32x4v kk = *(const f32x4v *)(kr + 4 * i);
+                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qv[4 * i], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qv[4 * i + 1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qv[4 * i + 2], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qv[4 * i + 3], d, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int t = tc + 16 * kt + 4 * g + i;
+                    const float x = t <= qlim ? d[i] * rinv : -INFINITY;
+                    sc[kt][i] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        if (m_new > -INFINITY) { // else no key of this token so far: nothing to add
+            const float f = m_run == -INFINITY ? 0.0f : expf(m_run - m_new);
+            m_run = m_new;
+            l_run *= f;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) o[dt] *= f;
+#pragma unroll
+            for (int kt = 0; kt < PA_KC / 16; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float e = sc[kt][i] == -INFINITY ? 0.0f : expf(sc[kt][i] - m_new);
+                    sc[kt][i] = e;
+                    l_run += e;
+                }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < PA_KC / 16; kt++) sc[kt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int kt = 0; kt < PA_KC / 16; kt++) {
+            if (kt < ntile) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float *vr = sv + (16 * kt + 4 * g + u) * KS + r;
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++)
+                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * dt], sc[kt][u], o[dt], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads(); // the next step's staging overwrites sk and sv
+    }
+    float l_tot = l_run + __shfl_xor(l_run, 16);
+    l_tot = l_tot + __shfl_xor(l_tot, 32);
+    const int S_m = (a.p0 + m) / a.att_sl + 1;
+    if (m0 + r >= a.M || s >= S_m) return; // no token here, or none of its positions in this slice
+    if (S_m == 1) { // the token's only slice: its output
+        float *dst = out + (size_t)m * a.dim + (size_t)h * HS + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) *(f32x4v *)(dst + 16 * dt) = o[dt] / l_tot;
+        return;
+    }
+    const size_t e0 = ((size_t)m * a.n_heads + h) * a.att_smax + s;
+    float *acc = a.att_acc + e0 * HS + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) *(f32x4v *)(acc + 16 * dt) = o[dt];
+    if (g == 0) {
+        a.att_ml[2 * e0] = m_run;
+        a.att_ml[2 * e0 + 1] = l_tot;
+    }
+}
+
 // causal attention of token m over positions 0 .. p0 + m, cut into slices of att_sl positions: block =
 // (kv head, token, slice) leaves the slice's running max, sum of exponentials and exp-weighted value sums
+// (the generic path, for head sizes and group sizes k_p_flash does not take)
 __global__ void __launch_bounds__(256) k_p_attention(ProwArgs a) {
     extern __shared__ __align__(16) float sm[];
     const int kvh = blockIdx.x, m = blockIdx.y, s = blockIdx.z, hs = a.head_size, kv_mul = a.n_heads / a.n_kv;
@@ -313,22 +464,34 @@ __global__ void __launch_bounds__(256) k_p_attention(ProwArgs a) {
     }
 }
 
-// merge of token m's slices: out[m][h*hs + e] = sum_s acc_s[e] * exp(max_s - max) / sum_s l_s * exp(max_s - max)
-__global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, float *out) {
-    const int m = blockIdx.x, hs = a.head_size, S = (a.p0 + m + a.att_sl) / a.att_sl;
-    for (int o = threadIdx.x; o < a.dim; o += blockDim.x) {
-        const int h = o / hs, e = o - h * hs;
+// merge of token m's S slices: with mx the largest slice max, w_s = exp(max_s - mx) / sum_k l_k exp(max_k - mx)
+// and out[m][h*hs + e] = sum_s acc_s[e] * w_s.  Tokens with one slice (S = 1) were written by k_p_flash,
+// unless `all` (the generic path, which leaves every token's slices).
+__global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, float *out, int all) {
+    extern __shared__ float wgt[]; // [n_heads][att_smax]
+    const int m = blockIdx.x, hs = a.head_size, S = (a.p0 + m) / a.att_sl + 1;
+    if (S == 1 && !all) return;
+    for (int h = threadIdx.x; h < a.n_heads; h += blockDim.x) {
         const float *ml = a.att_ml + ((size_t)m * a.n_heads + h) * a.att_smax * 2;
-        const float *acc = a.att_acc + ((size_t)m * a.n_heads + h) * a.att_smax * hs + e;
         float mx = ml[0];
         for (int k = 1; k < S; k++) mx = fmaxf(mx, ml[2 * k]);
-        float l = 0.0f, v = 0.0f;
+        float l = 0.0f;
         for (int k = 0; k < S; k++) {
             const float f = expf(ml[2 * k] - mx);
+            wgt[h * a.att_smax + k] = f;
             l += ml[2 * k + 1] * f;
-            v += acc[(size_t)k * hs] * f;
         }
-        out[(size_t)m * a.dim + o] = v / l;
+        const float il = 1.0f / l;
+        for (int k = 0; k < S; k++) wgt[h * a.att_smax + k] *= il;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < a.dim; o += blockDim.x) {
+        const int h = o / hs, e = o - h * hs;
+        const float *acc = a.att_acc + ((size_t)m * a.n_heads + h) * a.att_smax * hs + e;
+        const float *wh = wgt + h * a.att_smax;
+        float v = 0.0f;
+        for (int k = 0; k < S; k++) v += acc[(size_t)k * hs] * wh[k];
+        out[(size_t)m * a.dim + o] = v;
     }
 }
 
@@ -362,15 +525,28 @@ hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st) {
-    const int kv_mul = a.n_heads / a.n_kv;
-    if (kv_mul * a.head_size > 1024 || a.head_size % 4 || a.head_size > 128 || ((uintptr_t)a.q & 15) ||
-        ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) || a.kv_dim % 4 || a.dim % 4 || a.att_sl < ATT_SUB ||
-        a.att_smax < 1 || a.att_smax > PREFILL_ATT_SMAX || (a.p0 + a.M + a.att_sl - 1) / a.att_sl > a.att_smax)
+    const int kv_mul = a.n_heads / a.n_kv, hs = a.head_size;
+    if (kv_mul * hs > 1024 || hs % 4 || hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) ||
+        ((uintptr_t)a.vc & 15) || ((uintptr_t)out & 15) || ((uintptr_t)a.att_acc & 15) || a.kv_dim % 4 ||
+        a.dim % 4 || a.att_sl < ATT_SUB || a.att_sl % 16 || a.att_smax < 1 || a.att_smax > PREFILL_ATT_SMAX ||
+        (a.p0 + a.M + a.att_sl - 1) / a.att_sl > a.att_smax || a.n_heads % a.n_kv)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M, a.att_smax), dim3(256),
-                       attn_lds_floats(kv_mul, a.head_size) * 4, st, a);
+    const size_t merge_lds = (size_t)a.n_heads * a.att_smax * 4;
+    const bool flash = kv_mul <= 8 && (hs == 16 || hs == 32 || hs == 48 || hs == 64 || hs == 128);
+    if (flash) {
+        const dim3 grid(a.n_kv, (a.M + 15) / 16, a.att_smax);
+        const size_t lds = (size_t)2 * pa_kc(hs) * (hs + 4) * 4;
+#define PF_FLASH(HS_)                                                                                         \
+    if (hs == HS_) hipLaunchKernelGGL(k_p_flash<HS_>, grid, dim3(64 * kv_mul), lds, st, a, out);
+        PF_FLASH(16) PF_FLASH(32) PF_FLASH(48) PF_FLASH(64) PF_FLASH(128)
+#undef PF_FLASH
+    } else {
+        hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M, a.att_smax), dim3(256),
+                           attn_lds_floats(kv_mul, hs) * 4, st, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_p_attn_merge, dim3(a.M), dim3(256), 0, st, a, out);
+    if ((a.p0 + a.M - 1) / a.att_sl == 0 && flash) return hipSuccess; // every token has one slice
+    hipLaunchKernelGGL(k_p_attn_merge, dim3(a.M), dim3(256), merge_lds, st, a, out, flash ? 0 : 1);
     return hipGetLastError();
 }

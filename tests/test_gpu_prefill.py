@@ -116,3 +116,22 @@ def test_prefill_c3_shapes_two_layers(tmp_path):
     lg = m.prefill(ids)
     m.close()
     assert rel_err(lg, ref) < 2e-2
+
+
+@pytest.mark.parametrize("shape,n", [(("dim=896", "heads=14", "kv_heads=2"), 150), (("dim=512", "heads=4", "kv_heads=2"), 140),
+                                     (("dim=384", "heads=8", "kv_heads=8"), 70), (("dim=256", "heads=8", "kv_heads=2"), 90)])
+def test_prefill_attention_head_shapes(tmp_path, shape, n):
+    """head sizes 64 (7 query heads per kv head), 128, 48 (no grouping) and 32, one layer, prompts that span
+    two or three attention slices of 64 positions: prefill logits against as many decode steps.  The trimmed
+    head (256 rows) is smaller than the layer matrices, which the loader's staging area must still hold."""
+    p = synth("qwb", str(tmp_path / "h.qwb"), "tiny", 5, *shape, "hidden=256", "layers=1", "vocab=512", "head_k=256",
+              "max_seq=200")
+    a, b = pkg().Model(p, 200), pkg().Model(p, 200)
+    hid = a.head_ids
+    ids = [int(hid[v]) for v in np.random.default_rng(8).integers(0, len(hid), n)]
+    lg_pf = a.prefill(ids)
+    for pos, t in enumerate(ids):
+        lg_fw = b.forward(t, pos)
+    a.close()
+    b.close()
+    assert rel_err(lg_pf, lg_fw) < TOL
