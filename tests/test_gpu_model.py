@@ -250,3 +250,23 @@ def test_host_programs_match_reference_ids(name, extra, tmp_path):
         ref = golden(name, 256)
         n = min(len(got), len(ref))
         assert max(rel_err(a, b) for a, b in zip(got[:n], ref[:n])) < TOL
+
+
+TEXT = json.load(open(os.path.join(GOLDEN, "text_ref.json")))
+
+
+@pytest.mark.parametrize("name", sorted(TEXT))
+def test_host_programs_text_prompts_match_reference(name, tmp_path):
+    """text prompts through the hosts' tokenizers (Qwen chat template or raw, runq's BOS + dummy prefix), the
+    device loop, and the generated tokens printed as text: stdout byte for byte against the reference programs
+    run with the same synthetic models and tokenizers (tests/golden/make_tokenizers.py)"""
+    run = TEXT[name]
+    qwb = run["format"] == "qwb"
+    exe = os.path.join(PKG_DIR, "host", "qwen_hip" if qwb else "runq_hip")
+    if not os.path.exists(exe):
+        pytest.skip(f"{exe} not built")
+    model = synth(run["format"], str(tmp_path / f"m.{run['format']}"), *run["synth"])
+    tok = os.path.join(GOLDEN, "qwen_tok_synth.bin" if qwb else "llama_tok_synth.bin")
+    r = subprocess.run([exe, model, *run["args"], "-z", tok], capture_output=True, timeout=120)
+    assert r.returncode == 0, r.stderr.decode(errors="replace")
+    assert r.stdout == bytes.fromhex(run["stdout_hex"])
