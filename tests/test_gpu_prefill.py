@@ -24,8 +24,10 @@ def golden(name, n):
 
 @pytest.mark.parametrize("M,n,d,bits,rb", [(1, 96, 36, 4, 16), (7, 96, 36, 8, 16), (33, 896, 128, 4, 16),
                                            (64, 896, 64, 8, 16), (40, 4864, 32, 4, 8), (5, 256, 20, 4, 16),
-                                           (70, 128, 100, 4, 8)])
+                                           (70, 128, 100, 4, 8), (96, 64, 12288, 4, 16), (64, 896, 16384, 4, 16),
+                                           (64, 160, 16384, 8, 16)])
 def test_prefill_gemm_bit_exact_qwen(M, n, d, bits, rb):
+    """group counts below, at and above the 4 waves the K groups are dealt over; grids of 1024 tiles and more"""
     rng = np.random.default_rng(100 + M + n + d + bits)
     w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
     s = f16_scales(rng, d * n // 32)
@@ -38,7 +40,8 @@ def test_prefill_gemm_bit_exact_qwen(M, n, d, bits, rb):
         assert np.array_equal(y[m].view(np.uint32), o.view(np.uint32)), m
 
 
-@pytest.mark.parametrize("M,n,d,gs,rb", [(9, 288, 32, 32, 64), (33, 768, 96, 64, 64), (17, 768, 64, 32, 16)])
+@pytest.mark.parametrize("M,n,d,gs,rb", [(9, 288, 32, 32, 64), (33, 768, 96, 64, 64), (17, 768, 64, 32, 16),
+                                         (64, 288, 16384, 32, 64), (64, 192, 16384, 64, 64)])
 def test_prefill_gemm_bit_exact_runq(M, n, d, gs, rb):
     rng = np.random.default_rng(200 + M + n + d + gs)
     wq = rng.integers(-128, 128, size=d * n, dtype=np.int8)
