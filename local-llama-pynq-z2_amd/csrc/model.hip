@@ -839,7 +839,8 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
         pa.vc = m->vc + (size_t)l * m->ctx * kv;
         pa.bias = m->biases ? m->biases + (size_t)l * (dim + 2 * kv) : nullptr;
         pa.norm_w = attn_norm(m, l);
-        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, m->st));
+        // after the first layer, the previous down projection's output (in y) joins x before the norm
+        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, l > 0, m->st));
         g.W = Ly.qkv;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
         HIP_OR_FAIL("llm_prefill", launch_p_qkv(pa, m->st));
@@ -849,16 +850,15 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
         HIP_OR_FAIL("llm_prefill", launch_p_quant(pa, m->st));
         g.W = Ly.o;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
-        HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
         pa.norm_w = ffn_norm(m, l);
-        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, true, m->st)); // x += o output, then the FFN norm
         g.W = Ly.gu;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
         pa.gu_rb = Ly.gu.rb;
         HIP_OR_FAIL("llm_prefill", launch_p_swiglu_quant(pa, m->st));
         g.W = Ly.down;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
-        HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
+        if (l == I.n_layers - 1) HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
     }
     return 0;
 }

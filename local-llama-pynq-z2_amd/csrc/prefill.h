@@ -55,7 +55,7 @@ static inline void prefill_att_slices(int end, int *sl, int *smax) {
 
 hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStream_t st);
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st);
-hipError_t launch_p_norm_quant(const ProwArgs &a, hipStream_t st);
+hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st); // resid: x += y first
 hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_resid(const ProwArgs &a, hipStream_t st);

@@ -209,14 +209,21 @@ __global__ void __launch_bounds__(256) k_p_embed(ProwArgs a) {
     }
 }
 
-// rmsnorm (qwen.c:337-344, runq.c:394-407) of x[m], then int8 quantization (qwen.c:354-364 / runq.c:244-270)
+// rmsnorm (qwen.c:337-344, runq.c:394-407) of x[m], then int8 quantization (qwen.c:354-364 / runq.c:244-270).
+// With RESID the residual add of the previous GEMM comes first: x[m] += y[m] (qwen.c:551, 565; runq.c:575-577,
+// 603-605), stored back, then normalized.
+template <bool RESID>
 __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     extern __shared__ __align__(16) float sv[]; // dim floats + 4 per wave
     const int m = blockIdx.x, n = a.dim;
-    const float *x = a.x + (size_t)m * n;
+    float *x = a.x + (size_t)m * n;
     float part = 0.0f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
+        float v = x[i];
+        if constexpr (RESID) {
+            v = v + a.y[(size_t)m * n + i];
+            x[i] = v;
+        }
         sv[i] = v;
         part += v * v;
     }
@@ -526,9 +533,10 @@ hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(k_p_embed, dim3(a.M), dim3(256), 0, st, a);
     return hipGetLastError();
 }
-hipError_t launch_p_norm_quant(const ProwArgs &a, hipStream_t st) {
+hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st) {
     if (a.dim % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_p_norm_quant, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
+    if (resid) hipLaunchKernelGGL(k_p_norm_quant<true>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
+    else hipLaunchKernelGGL(k_p_norm_quant<false>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
     return hipGetLastError();
 }
 hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st) {
