@@ -17,7 +17,7 @@ import unicodedata
 
 import pytest
 
-from helpers import GOLDEN, PKG_DIR
+from helpers import GOLDEN, PKG_DIR, REF_DIR, synth
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 TOOL = os.path.join(PKG_DIR, "host", "tok_tool")
@@ -123,3 +123,20 @@ def test_llama_matches_reference_live():
     lines = b"\n".join(" ".join(map(str, ids)).encode() for ids in mine)
     lines += b"\n" + " ".join(map(str, range(int(v)))).encode()
     assert run([tool(), "llama", LTOK, v, "dec"], lines) == run([REF_LLAMA, LTOK, v, "dec"], lines)
+
+
+def test_reference_qwen_links_this_tokenizer(tmp_path):
+    """the reference's qwen.c built unchanged with host/qwen_tokenizer.c in place of its tokenizer.c
+    (oracle/Makefile: _ref/qwen_ourtok) prints the same text as with its own, chat template and raw, greedy and
+    sampled, on a synthetic model (CPU forward of the reference)"""
+    ours, theirs = os.path.join(REF_DIR, "qwen_ourtok"), os.path.join(REF_DIR, "qwen")
+    if not (os.path.exists(ours) and os.path.exists(theirs)):
+        pytest.skip("oracle/_ref/qwen_ourtok or qwen is not built (make -C oracle ref)")
+    model = synth("qwb", str(tmp_path / "m.qwb"), "tiny", 5, "max_seq=256")
+    for args in (["-i", "Write a short poem about the sea.", "-m", "chat", "-t", "0"],
+                 ["-i", "café <|im_end|> 12345\n\tend", "-m", "raw", "-t", "0.9", "-p", "0.9", "-s", "3"]):
+        cmd = [model, *args, "-n", "24", "-c", "256", "-z", QTOK]
+        a = subprocess.run([ours, *cmd], capture_output=True, timeout=300)
+        b = subprocess.run([theirs, *cmd], capture_output=True, timeout=300)
+        assert a.returncode == 0 and b.returncode == 0, (a.stderr, b.stderr)
+        assert a.stdout == b.stdout and len(a.stdout) > 1
