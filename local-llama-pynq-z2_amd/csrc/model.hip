@@ -79,7 +79,7 @@ struct llm_model {
     hipGraphExec_t g_plain_s = nullptr, g_hist_s = nullptr;
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, prefill_on = 1;
-    float *pf_x = nullptr, *pf_y = nullptr, *pf_q = nullptr, *pf_z = nullptr, *pf_s = nullptr;
+    float *pf_x = nullptr, *pf_y = nullptr, *pf_q = nullptr, *pf_s = nullptr;
     float *pf_ml = nullptr, *pf_acc = nullptr; // attention slice partials
     int8_t *pf_a = nullptr;
     int *pf_ids = nullptr;
@@ -775,12 +775,12 @@ int prefill_alloc(llm_model *m, int M) {
     if (M <= m->pf_cap) return 0;
     const llm_info &I = m->info;
     const int dim = I.dim, hid = I.hidden_dim, rows = std::max(dim + 2 * m->kv_dim, 2 * hid), wmax = std::max(dim, hid);
-    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
+    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_s,
                     (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
         if (p) hipFree(p);
     m->pf_cap = 0;
     if (hipMalloc(&m->pf_x, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_y, (size_t)M * rows * 4) != hipSuccess ||
-        hipMalloc(&m->pf_q, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_z, (size_t)M * dim * 4) != hipSuccess ||
+        hipMalloc(&m->pf_q, (size_t)M * dim * 4) != hipSuccess ||
         hipMalloc(&m->pf_s, (size_t)M * (wmax / m->gs) * 4) != hipSuccess ||
         hipMalloc(&m->pf_a, (size_t)M * wmax) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess ||
         hipMalloc(&m->pf_ml, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * 2 * 4) != hipSuccess ||
@@ -844,10 +844,7 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
         g.W = Ly.qkv;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
         HIP_OR_FAIL("llm_prefill", launch_p_qkv(pa, m->st));
-        HIP_OR_FAIL("llm_prefill", launch_p_attention(pa, m->pf_z, m->st));
-        pa.z = m->pf_z;
-        pa.width = dim;
-        HIP_OR_FAIL("llm_prefill", launch_p_quant(pa, m->st));
+        HIP_OR_FAIL("llm_prefill", launch_p_attention(pa, m->st)); // the o projection's int8 input
         g.W = Ly.o;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
         pa.norm_w = ffn_norm(m, l);
@@ -888,7 +885,7 @@ void free_model(llm_model *m) {
         if (g) hipGraphExecDestroy(g);
     for (void *p : m->allocs) hipFree(p);
     if (m->hist) hipFree(m->hist);
-    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_z, (void *)m->pf_s,
+    for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_s,
                     (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
         if (p) hipFree(p);
     if (m->st) hipStreamDestroy(m->st);

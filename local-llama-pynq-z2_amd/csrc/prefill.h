@@ -32,10 +32,8 @@ struct ProwArgs {           // per-token elementwise kernels
     const float *rope_cos, *rope_sin; // [ctx][hs/2]
     float *q;               // [M][dim]
     float *kc, *vc;         // this layer's caches [ctx][kv_dim]
-    const float *z;         // [M][width] input of k_p_quant
-    int8_t *oq;             // [M][width] quantized output
+    int8_t *oq;             // [M][width] quantized output (the next GEMM's input)
     float *os;              // [M][width / gs]
-    int width;              // row width of z / oq for k_p_quant
     int n_heads, n_kv;
     // attention slices: positions of token m in slices of att_sl, at most att_smax per token; partials
     // ml [M][n_heads][att_smax][2] (max, sum of exp) and acc [M][n_heads][att_smax][hs]
@@ -56,8 +54,7 @@ static inline void prefill_att_slices(int end, int *sl, int *smax) {
 hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStream_t st);
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st); // resid: x += y first
-hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_resid(const ProwArgs &a, hipStream_t st);
 hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st);
-hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st); // slices, then their merge
+hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st); // slices, merge; int8 output in oq/os

@@ -236,15 +236,6 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
 }
 
-// int8 quantization of z[m] (the attention output, qwen.c:549 / runq.c:571)
-__global__ void __launch_bounds__(256) k_p_quant(ProwArgs a) {
-    extern __shared__ __align__(16) float sv[];
-    const int m = blockIdx.x, n = a.width;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.z[(size_t)m * n + i];
-    __syncthreads();
-    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
-}
-
 // QKV rows of token m: bias (qwen.c:521-522), RoPE at position p0 + m (qwen.c:478-488 NeoX pairs; runq.c:506-521
 // interleaved pairs), q to q[m], k and v into the caches.  Logical rows follow the fused matrix's order.
 __global__ void __launch_bounds__(256) k_p_qkv(ProwArgs a) {
@@ -295,15 +286,34 @@ __global__ void __launch_bounds__(256) k_p_resid(ProwArgs a) {
 // come in row-blocks of gu_rb: gu_rb/2 gate rows, then the matching up rows.
 __global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
     extern __shared__ __align__(16) float sv[];
-    const int m = blockIdx.x, hid = a.hidden, hb = a.gu_rb / 2;
+    const int m = blockIdx.x, hid = a.hidden, hb = a.gu_rb / 2; // hb: a multiple of 4
     const float *y = a.y + (size_t)m * 2 * hid;
-    for (int j = threadIdx.x; j < hid; j += blockDim.x) {
-        const int b = j / hb, r = j - b * hb;
-        float g = y[b * a.gu_rb + r];
-        const float u = y[b * a.gu_rb + hb + r];
-        const float sig = 1.0f / (1.0f + expf(-g));
-        g = g * sig;
-        sv[j] = g * u;
+    // 16-byte loads of 4 gate and the 4 matching up values, V pairs per thread issued before any is used
+    constexpr int V = 8;
+    const int step = 4 * blockDim.x;
+    for (int j0 = 4 * threadIdx.x; j0 < hid; j0 += V * step) {
+        float4 g4[V], u4[V];
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const int j = min(j0 + k * step, hid - 4), b = j / hb, r = j - b * hb;
+            g4[k] = *(const float4 *)(y + b * a.gu_rb + r);
+            u4[k] = *(const float4 *)(y + b * a.gu_rb + hb + r);
+        }
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const int j = j0 + k * step;
+            if (j < hid) {
+                const float g[4] = {g4[k].x, g4[k].y, g4[k].z, g4[k].w}, u[4] = {u4[k].x, u4[k].y, u4[k].z, u4[k].w};
+                float h[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float sig = 1.0f / (1.0f + expf(-g[e]));
+                    const float gs = g[e] * sig;
+                    h[e] = gs * u[e];
+                }
+                *(float4 *)(sv + j) = make_float4(h[0], h[1], h[2], h[3]);
+            }
+        }
     }
     __syncthreads();
     block_quantize(sv, hid, a.gs, a.qflavor, a.oq + (size_t)m * hid, a.os + (size_t)m * (hid / a.gs));
@@ -329,8 +339,11 @@ __host__ __device__ constexpr int pa_kc(int hs) { return hs >= 128 ? 32 : 64; }
 //     own probability; D lane = O[token r][16 dt + 4g + i].
 // The online softmax (running max and sum per token) therefore needs no data movement except the max over
 // the four lanes of a token.
+// With `direct`, a token whose positions all fall in slice 0 gets its output here, normalized and quantized
+// to int8 for the o projection (a group of gs values lies inside one head: hs % gs == 0); every other token
+// leaves its slice partials for k_p_attn_merge.
 template <int HS>
-__global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, float *out) {
+__global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
     constexpr int H4 = HS / 4, KS = HS + 4, DT = HS / 16, PA_KC = pa_kc(HS);
     extern __shared__ __align__(16) float sm[];
     float *sk = sm, *sv = sm + PA_KC * KS; // [PA_KC][KS] each
@@ -436,13 +449,44 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, float *out) {
     float l_tot = l_run + __shfl_xor(l_run, 16);
     l_tot = l_tot + __shfl_xor(l_tot, 32);
     const int S_m = (a.p0 + m) / a.att_sl + 1;
-    if (m0 + r >= a.M || s >= S_m) return; // no token here, or none of its positions in this slice
-    if (S_m == 1) { // the token's only slice: its output
-        float *dst = out + (size_t)m * a.dim + (size_t)h * HS + 4 * g;
+    const bool tok_ok = m0 + r < a.M;
+    if (direct && s == 0) {
+        // the 4 lanes of token r hold its dims 16 dt + 4 g + i; a group of gs dims is gs / 16 tiles dt of
+        // those lanes: its max over the lane's values, then over the 4 lanes (every lane takes part)
+        const bool mine = tok_ok && S_m == 1;
+        const int tiles = a.gs / 16; // 2 or 4, uniform
+        f32x4v val[DT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) *(f32x4v *)(dst + 16 * dt) = o[dt] / l_tot;
-        return;
+        for (int dt = 0; dt < DT; dt++) val[dt] = o[dt] / l_tot;
+        int8_t *oq = a.oq + (size_t)m * a.dim + (size_t)h * HS + 4 * g;
+        float *os = a.os + ((size_t)m * a.dim + (size_t)h * HS) / a.gs;
+#pragma unroll
+        for (int g0 = 0; g0 < DT; g0++) {
+            if (g0 % tiles) continue; // not the first tile of a group
+            float mx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (k < tiles && g0 + k < DT)
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(val[g0 + k].x), fabsf(val[g0 + k].y)),
+                                         fmaxf(fabsf(val[g0 + k].z), fabsf(val[g0 + k].w))));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float scale = quant_scale(mx, a.qflavor), inv = quant_inv(scale);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (mine && k < tiles && g0 + k < DT) {
+                    const f32x4v v = val[g0 + k];
+                    const uint32_t b0 = (uint8_t)quant_one(v.x, scale, inv, a.qflavor);
+                    const uint32_t b1 = (uint8_t)quant_one(v.y, scale, inv, a.qflavor);
+                    const uint32_t b2 = (uint8_t)quant_one(v.z, scale, inv, a.qflavor);
+                    const uint32_t b3 = (uint8_t)quant_one(v.w, scale, inv, a.qflavor);
+                    *(uint32_t *)(oq + 16 * (g0 + k)) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                }
+            if (mine && g == 0) os[16 * g0 / a.gs] = scale;
+        }
+        if (S_m == 1) return;
     }
+    if (!tok_ok || s >= S_m) return; // no token here, or none of its positions in this slice
     const size_t e0 = ((size_t)m * a.n_heads + h) * a.att_smax + s;
     float *acc = a.att_acc + e0 * HS + 4 * g;
 #pragma unroll
@@ -482,10 +526,11 @@ __global__ void __launch_bounds__(256) k_p_attention(ProwArgs a) {
 }
 
 // merge of token m's S slices: with mx the largest slice max, w_s = exp(max_s - mx) / sum_k l_k exp(max_k - mx)
-// and out[m][h*hs + e] = sum_s acc_s[e] * w_s.  Tokens with one slice (S = 1) were written by k_p_flash,
-// unless `all` (the generic path, which leaves every token's slices).
-__global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, float *out, int all) {
-    extern __shared__ float wgt[]; // [n_heads][att_smax]
+// and out[h*hs + e] = sum_s acc_s[e] * w_s, then the row quantized to int8 for the o projection (qwen.c:549,
+// runq.c:571).  Tokens with one slice were done by k_p_flash, unless `all` (then every token is merged here).
+__global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
+    extern __shared__ __align__(16) float sm[]; // dim floats of the row, then [n_heads][att_smax] weights
+    float *row = sm, *wgt = sm + a.dim;
     const int m = blockIdx.x, hs = a.head_size, S = (a.p0 + m) / a.att_sl + 1;
     if (S == 1 && !all) return;
     // fixed-trip loops with the slice count as a predicate: every load of a row is issued before the first
@@ -525,8 +570,10 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, float *out, in
 #pragma unroll
         for (int k = 0; k < PREFILL_ATT_SMAX; k++)
             if (k < S) v += x[k] * wh[k];
-        out[(size_t)m * a.dim + o] = v;
+        row[o] = v;
     }
+    __syncthreads();
+    block_quantize(row, a.dim, a.gs, a.qflavor, a.oq + (size_t)m * a.dim, a.os + (size_t)m * (a.dim / a.gs));
 }
 
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
@@ -537,11 +584,6 @@ hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st) {
     if (a.dim % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
     if (resid) hipLaunchKernelGGL(k_p_norm_quant<true>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
     else hipLaunchKernelGGL(k_p_norm_quant<false>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
-    return hipGetLastError();
-}
-hipError_t launch_p_quant(const ProwArgs &a, hipStream_t st) {
-    if (a.width % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_p_quant, dim3(a.M), dim3(256), (size_t)a.width * 4, st, a);
     return hipGetLastError();
 }
 hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st) {
@@ -555,24 +597,26 @@ hipError_t launch_p_resid(const ProwArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st) {
-    if (a.hidden % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
+    if (a.hidden % 4 || a.gu_rb % 8 || ((uintptr_t)a.oq & 3) || ((uintptr_t)a.y & 15)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_p_swiglu_quant, dim3(a.M), dim3(256), (size_t)a.hidden * 4, st, a);
     return hipGetLastError();
 }
-hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st) {
+hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv, hs = a.head_size;
     if (kv_mul * hs > 1024 || hs % 4 || hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) ||
-        ((uintptr_t)a.vc & 15) || ((uintptr_t)out & 15) || ((uintptr_t)a.att_acc & 15) || a.kv_dim % 4 ||
-        a.dim % 4 || a.att_sl < ATT_SUB || a.att_sl % 16 || a.att_smax < 1 || a.att_smax > PREFILL_ATT_SMAX ||
-        (a.p0 + a.M + a.att_sl - 1) / a.att_sl > a.att_smax || a.n_heads % a.n_kv)
+        ((uintptr_t)a.vc & 15) || ((uintptr_t)a.oq & 3) || ((uintptr_t)a.att_acc & 15) || a.kv_dim % 4 ||
+        a.dim % 4 || a.dim % a.gs || a.att_sl < ATT_SUB || a.att_sl % 16 || a.att_smax < 1 ||
+        a.att_smax > PREFILL_ATT_SMAX || (a.p0 + a.M + a.att_sl - 1) / a.att_sl > a.att_smax || a.n_heads % a.n_kv)
         return hipErrorInvalidValue;
-    const size_t merge_lds = (size_t)a.n_heads * a.att_smax * 4;
+    const size_t merge_lds = ((size_t)a.dim + (size_t)a.n_heads * a.att_smax) * 4;
     const bool flash = kv_mul <= 8 && (hs == 16 || hs == 32 || hs == 48 || hs == 64 || hs == 128);
+    // single-slice tokens quantized by the slice kernel when a quantization group stays inside one head
+    const int direct = flash && hs % a.gs == 0 && (a.gs == 32 || a.gs == 64);
     if (flash) {
         const dim3 grid(a.n_kv, (a.M + 15) / 16, a.att_smax);
         const size_t lds = (size_t)2 * pa_kc(hs) * (hs + 4) * 4;
 #define PF_FLASH(HS_)                                                                                         \
-    if (hs == HS_) hipLaunchKernelGGL(k_p_flash<HS_>, grid, dim3(64 * kv_mul), lds, st, a, out);
+    if (hs == HS_) hipLaunchKernelGGL(k_p_flash<HS_>, grid, dim3(64 * kv_mul), lds, st, a, direct);
         PF_FLASH(16) PF_FLASH(32) PF_FLASH(48) PF_FLASH(64) PF_FLASH(128)
 #undef PF_FLASH
     } else {
@@ -581,7 +625,7 @@ hipError_t launch_p_attention(const ProwArgs &a, float *out, hipStream_t st) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if ((a.p0 + a.M - 1) / a.att_sl == 0 && flash) return hipSuccess; // every token has one slice
-    hipLaunchKernelGGL(k_p_attn_merge, dim3(a.M), dim3(256), merge_lds, st, a, out, flash ? 0 : 1);
+    if ((a.p0 + a.M - 1) / a.att_sl == 0 && direct) return hipSuccess; // every token has one slice
+    hipLaunchKernelGGL(k_p_attn_merge, dim3(a.M), dim3(256), merge_lds, st, a, direct ? 0 : 1);
     return hipGetLastError();
 }

@@ -121,16 +121,21 @@ def test_prefill_c3_shapes_two_layers(tmp_path):
     assert rel_err(lg, ref) < 2e-2
 
 
-@pytest.mark.parametrize("shape,n", [(("dim=896", "heads=14", "kv_heads=2"), 150), (("dim=512", "heads=4", "kv_heads=2"), 140),
-                                     (("dim=384", "heads=8", "kv_heads=8"), 70), (("dim=256", "heads=8", "kv_heads=2"), 90)])
-def test_prefill_attention_head_shapes(tmp_path, shape, n):
-    """head sizes 64 (7 query heads per kv head), 128, 48 (no grouping) and 32, one layer, prompts that span
-    two or three attention slices of 64 positions: prefill logits against as many decode steps.  The trimmed
-    head (256 rows) is smaller than the layer matrices, which the loader's staging area must still hold."""
-    p = synth("qwb", str(tmp_path / "h.qwb"), "tiny", 5, *shape, "hidden=256", "layers=1", "vocab=512", "head_k=256",
-              "max_seq=200")
+@pytest.mark.parametrize("fmt,shape,n", [("qwb", ("dim=896", "heads=14", "kv_heads=2"), 150),
+                                         ("qwb", ("dim=512", "heads=4", "kv_heads=2"), 140),
+                                         ("qwb", ("dim=384", "heads=8", "kv_heads=8"), 70),
+                                         ("qwb", ("dim=256", "heads=8", "kv_heads=2"), 90),
+                                         ("bin", ("dim=256", "heads=4", "kv_heads=4", "gs=64"), 150)])
+def test_prefill_attention_head_shapes(tmp_path, fmt, shape, n):
+    """head sizes 64 (7 query heads per kv head), 128, 48 (no grouping) and 32, and a runq model with
+    quantization groups of 64 (one group per head), one layer, prompts that span two or three attention
+    slices of 64 positions: prefill logits against as many decode steps.  The attention kernels write the o
+    projection's int8 input themselves (groups inside a head) or through the slice merge.  The trimmed head
+    (256 rows) is smaller than the layer matrices, which the loader's staging area must still hold."""
+    extra = ["hidden=256", "layers=1", "vocab=512", "max_seq=200"] + (["head_k=256"] if fmt == "qwb" else [])
+    p = synth(fmt, str(tmp_path / f"h.{fmt}"), "tiny", 5, *shape, *extra)
     a, b = pkg().Model(p, 200), pkg().Model(p, 200)
-    hid = a.head_ids
+    hid = a.head_ids if fmt == "qwb" else np.arange(512)
     ids = [int(hid[v]) for v in np.random.default_rng(8).integers(0, len(hid), n)]
     lg_pf = a.prefill(ids)
     for pos, t in enumerate(ids):
