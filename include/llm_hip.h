@@ -59,6 +59,16 @@ int llm_forward(llm_model *m, int token, int pos, float *logits);
 int llm_generate(llm_model *m, const int *prompt, int n_prompt, int max_new, int *out, float *logits,
                  llm_timing *timing);
 
+/* The token loop continued from an earlier llm_generate / llm_continue, for multi-turn dialogs (runq's chat
+ * loop, runq.c:1055-1140): the n tokens are forced at positions pos0 .. pos0 + n - 1 over the KV cache that
+ * earlier calls left below pos0, then up to max_new tokens are generated (argmax, or the sampler of
+ * llm_set_sampler) until stop_id is generated (not stored; -1: the format's stop ids, as llm_generate) or
+ * the context is full.  Returns the number of generated ids written to out, or -1.  Steps run in batches,
+ * so after a stop the device's sampler state may have advanced past the stop's draw: a caller that
+ * continues a sampled stream sets the state it wants with llm_set_sampler first. */
+int llm_continue(llm_model *m, int pos0, const int *tokens, int n, int max_new, int stop_id, int *out,
+                 llm_timing *timing);
+
 /* Decode throughput: replays the captured step graph `steps` times from the current position (after a
  * prompt was forced by llm_generate or llm_forward) with no host round trips, and returns the elapsed time
  * of exactly those replays in *ms (HIP events on the library's stream).  With the sampler on

@@ -69,6 +69,7 @@ def lib():
     L.llm_head_ids.argtypes = [vp]
     L.llm_forward.argtypes = [vp, i32, i32, vp]
     L.llm_generate.argtypes = [vp, vp, i32, i32, vp, vp, C.POINTER(LlmTiming)]
+    L.llm_continue.argtypes = [vp, i32, vp, i32, i32, i32, vp, C.POINTER(LlmTiming)]
     L.llm_decode_replay.argtypes = [vp, i32, C.POINTER(C.c_double)]
     L.llm_profile.argtypes = [vp, i32, C.POINTER(LlmKernelStat), i32]
     L.llm_profile_graph.argtypes = [vp, i32, i32, C.POINTER(LlmKernelStat), i32, C.POINTER(C.c_double)]
@@ -212,6 +213,17 @@ class Model:
         if logits:
             res["logits"] = lg[:t.n_forward * self.info.n_logits].reshape(t.n_forward, self.info.n_logits)
         return res
+
+    def continue_at(self, pos0, tokens, max_new, stop_id=-1):
+        """the tokens forced from position pos0 over the cache earlier calls left, then up to max_new generated
+        ids until stop_id (-1: the format's stop ids)"""
+        p = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty(max_new, np.int32)
+        t = LlmTiming()
+        n = self.L.llm_continue(self.h, pos0, _ptr(p), len(p), max_new, stop_id, _ptr(out), C.byref(t))
+        if n < 0:
+            raise RuntimeError("llm_continue failed")
+        return {"ids": out[:n].copy(), "timing": t}
 
     def decode_replay(self, steps):
         ms = C.c_double(0)

@@ -860,19 +860,20 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     return 0;
 }
 
-// All n prompt positions, then the head of the last one: logits, argmax partials, and (finalize) its argmax
-// into gen[n - 1].  Afterwards the step state is position n - 1, as after n forward() calls.
-int prefill_all(llm_model *m, const int *ids, int n, bool sampled = false) {
+// Positions pos0 .. pos0 + n - 1 (the cache below pos0 kept), then the head of the last one: logits, argmax
+// partials, and (finalize) its argmax into gen[pos0 + n - 1].  Afterwards the step state is position
+// pos0 + n - 1, as after those forward() calls.
+int prefill_all(llm_model *m, const int *ids, int n, bool sampled = false, int pos0 = 0) {
     if (prefill_alloc(m, std::min(n, PREFILL_CHUNK))) return -1;
-    for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
-        const int M = std::min(PREFILL_CHUNK, n - p0);
-        if (prefill_chunk(m, ids + p0, p0, M)) return -1;
-        if (p0 + M == n)
+    for (int i = 0; i < n; i += PREFILL_CHUNK) {
+        const int M = std::min(PREFILL_CHUNK, n - i);
+        if (prefill_chunk(m, ids + i, pos0 + i, M)) return -1;
+        if (i + M == n)
             HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->x, m->pf_x + (size_t)(M - 1) * m->info.dim,
                                                       (size_t)m->info.dim * 4, hipMemcpyDeviceToDevice, m->st));
     }
-    HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->tokens, ids, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
-    if (set_ctrl(m, n - 1, ids[n - 1], 0, 0)) return -1;
+    HIP_OR_FAIL("llm_prefill", hipMemcpyAsync(m->tokens + pos0, ids, (size_t)n * 4, hipMemcpyHostToDevice, m->st));
+    if (set_ctrl(m, pos0 + n - 1, ids[n - 1], 0, 0)) return -1;
     HIP_OR_FAIL("llm_prefill", launch_head(m, false));
     if (sampled) HIP_OR_FAIL("llm_prefill", launch_sampler(m));
     HIP_OR_FAIL("llm_prefill", launch_finalize(m));
@@ -978,14 +979,17 @@ static double now_ms() {
     return t.tv_sec * 1e3 + t.tv_nsec / 1e6;
 }
 
-extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int max_new, int *out, float *logits,
-                            llm_timing *timing) {
-    if (!m || !prompt || n_prompt < 1 || max_new < 1) {
+// The token loop from position pos0: the n_prompt tokens forced at pos0 .. pos0 + n_prompt - 1 (the KV cache
+// below pos0 is what earlier calls left), then up to max_new generated tokens.  stop_id >= 0 replaces the
+// format's stop ids.  Positions are absolute: prompt, tokens and gen are indexed by position.
+static int generate_from(llm_model *m, int pos0, const int *prompt, int n_prompt, int max_new, int stop_id, int *out,
+                         float *logits, llm_timing *timing) {
+    if (!m || !prompt || n_prompt < 1 || max_new < 1 || pos0 < 0 || (logits && pos0 > 0)) {
         fprintf(stderr, "llm_generate: bad arguments\n");
         return -1;
     }
-    if (n_prompt > m->ctx) { // a prompt of exactly ctx positions still yields one token from the last
-        fprintf(stderr, "prompt (%d tokens) does not fit -c %d\n", n_prompt, m->ctx);
+    if (pos0 + n_prompt > m->ctx) { // a prompt ending at the last position still yields one token from it
+        fprintf(stderr, "prompt (%d tokens from position %d) does not fit -c %d\n", n_prompt, pos0, m->ctx);
         return -1;
     }
     for (int i = 0; i < n_prompt; i++)
@@ -1003,15 +1007,16 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
         }
     }
     if (!*g && capture(m, hist, g, 0, smp)) return -1;
-    HIP_OR_FAIL("llm_generate", hipMemcpy(m->prompt, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
-    if (set_ctrl(m, -1, 0, n_prompt, 1)) return -1;
+    HIP_OR_FAIL("llm_generate", hipMemcpy(m->prompt + pos0, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    const int end_prompt = pos0 + n_prompt; // positions below take their token from the prompt
+    if (set_ctrl(m, pos0 - 1, 0, end_prompt, 1)) return -1;
     // positions: the prompt, then one per generated token, within the context
-    const int last_pos = n_prompt - 1 + max_new - 1 < m->ctx - 1 ? n_prompt - 1 + max_new - 1 : m->ctx - 1;
+    const int last_pos = std::min(end_prompt - 1 + max_new - 1, m->ctx - 1);
     const double t0 = now_ms();
     if (m->prefill_on && !hist && n_prompt > 1) {
         // the prompt in one batched pass; the first decode step then finishes its last position's argmax
-        if (prefill_all(m, prompt, n_prompt, smp)) return -1;
-        if (set_ctrl(m, n_prompt - 1, prompt[n_prompt - 1], n_prompt, 1)) return -1;
+        if (prefill_all(m, prompt, n_prompt, smp, pos0)) return -1;
+        if (set_ctrl(m, end_prompt - 1, prompt[n_prompt - 1], end_prompt, 1)) return -1;
     } else {
         for (int p = 0; p < n_prompt; p++) HIP_OR_FAIL("llm_generate", hipGraphLaunch(*g, m->st));
     }
@@ -1021,7 +1026,7 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
     // gen[p] is the argmax of position p; generated token k is gen[n_prompt - 1 + k].  Steps run in batches,
     // then the batch's tokens are read back and checked for stop ids (qwen.c:684, runq.c:1016).
     const int batch = 16;
-    int ran = n_prompt - 1, checked = n_prompt - 1, n_out = 0, used = n_prompt - 1;
+    int ran = end_prompt - 1, checked = end_prompt - 1, n_out = 0, used = end_prompt - 1;
     bool done = false;
     while (!done) {
         const int upto = ran + batch < last_pos ? ran + batch : last_pos;
@@ -1034,7 +1039,8 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
         for (int p = checked; p <= ran; p++) {
             const int next = gen[p];
             used = p;
-            const bool stop = m->kind == 0 ? (next == 151645 || next == 151643) : next == 1;
+            const bool stop = stop_id >= 0 ? next == stop_id
+                                           : m->kind == 0 ? (next == 151645 || next == 151643) : next == 1;
             if (stop) { done = true; break; }
             out[n_out++] = next;
             if (n_out >= max_new || p >= m->ctx - 1) { done = true; break; }
@@ -1047,7 +1053,7 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
     if (timing) {
         timing->n_prompt = n_prompt;
         timing->n_generated = n_out;
-        timing->n_forward = pos + 1;
+        timing->n_forward = pos + 1 - pos0;
         timing->prompt_ms = t1 - t0;
         timing->decode_ms = t2 - t1;
     }
@@ -1055,6 +1061,16 @@ extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int m
         HIP_OR_FAIL("llm_generate", hipMemcpy(logits, m->hist, (size_t)(pos + 1) * m->info.n_logits * 4,
                                               hipMemcpyDeviceToHost));
     return n_out;
+}
+
+extern "C" int llm_generate(llm_model *m, const int *prompt, int n_prompt, int max_new, int *out, float *logits,
+                            llm_timing *timing) {
+    return generate_from(m, 0, prompt, n_prompt, max_new, -1, out, logits, timing);
+}
+
+extern "C" int llm_continue(llm_model *m, int pos0, const int *tokens, int n, int max_new, int stop_id, int *out,
+                            llm_timing *timing) {
+    return generate_from(m, pos0, tokens, n, max_new, stop_id, out, nullptr, timing);
 }
 
 extern "C" int llm_decode_replay(llm_model *m, int steps, double *ms) {

@@ -43,6 +43,14 @@ TEXT_RUNS = [
     ("runq_greedy", "bin", ["vocab=512"], "runq", ["-i", "Once upon a time", "-n", "48", "-t", "0"]),
     ("runq_sampled", "bin", ["vocab=512"], "runq", ["-i", "The quick brown fox", "-n", "40", "-t", "0.8", "-p", "0.9",
                                                    "-s", "5"]),
+    # runq.c's chat loop, turns from stdin.  Seed 1 at t 1.0 ends two replies with EOS; 155 positions stop
+    # inside the third turn's prompt.  (A sampled run of hundreds of coins over 512 near-uniform rows is likely
+    # to meet a coin within fp32 rounding of a cdf boundary somewhere: the sampler's bar, test_gpu_sample.py.)
+    ("runq_chat_sampled", "bin", ["vocab=512", "max_seq=512"], "runq",
+     ["-m", "chat", "-y", "Be brief.", "-i", "Hello there", "-n", "155", "-t", "1.0", "-p", "0.95", "-s", "1"],
+     "How are you?\nTell me more\nBye\n"),
+    ("runq_chat_greedy", "bin", ["vocab=512", "max_seq=512"], "runq", ["-m", "chat", "-n", "200", "-t", "0"],
+     "Be brief.\nHello there\nHow are you?\n"),
 ]
 QWEN_SPLIT = (r"(?i:'s|'t|'re|'ve|'m|'ll|'d)|[^\r\n\p{L}\p{N}]?\p{L}+|\p{N}| ?[^\s\p{L}\p{N}]+[\r\n]*|"
               r"\s*[\r\n]+|\s+(?!\S)|\s+")
@@ -255,14 +263,16 @@ def text_runs():
     import tempfile
     out = {}
     d = tempfile.mkdtemp()
-    for name, fmt, over, prog, args in TEXT_RUNS:
+    for name, fmt, over, prog, args, *stdin in TEXT_RUNS:
         model = os.path.join(d, f"{name}.{fmt}")
         seed = "5" if name == "qwen_chat" else "1"
         subprocess.run([SYNTH, fmt, model, "tiny", seed, *over], check=True, capture_output=True)
         tok = os.path.join(HERE, "qwen_tok_synth.bin" if fmt == "qwb" else "llama_tok_synth.bin")
+        feed = stdin[0].encode() if stdin else b""
         r = subprocess.run([os.path.join(REPO, "oracle", "_ref", prog), model, *args, "-z", tok], capture_output=True,
-                           check=True, timeout=300)
-        out[name] = {"format": fmt, "synth": ["tiny", seed, *over], "args": args, "stdout_hex": r.stdout.hex()}
+                           check=True, timeout=300, input=feed)
+        out[name] = {"format": fmt, "synth": ["tiny", seed, *over], "args": args, "stdin": feed.decode(),
+                     "stdout_hex": r.stdout.hex()}
     json.dump(out, open(os.path.join(HERE, "text_ref.json"), "w"), indent=1)
 
 

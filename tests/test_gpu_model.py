@@ -178,6 +178,27 @@ def test_in_graph_profile_accounts_for_the_step_and_restores_the_position():
     assert list(r["ids"]) == meta["ids"]
 
 
+@pytest.mark.parametrize("name,prefill", [("qwb", True), ("qwb", False), ("bin", True)])
+def test_continue_extends_a_generation(name, prefill):
+    """llm_continue over the cache an earlier call left: a greedy generation split in two (the first part's
+    tokens fed back as the second call's prompt, from the position after the first prompt) gives the same ids
+    as one llm_generate call; a stop id ends the second call at its first occurrence"""
+    meta = META[name]
+    runq = name == "bin"
+    m = pkg().Model(os.path.join(GOLDEN, "tiny.bin" if runq else "tiny.qwb"), 1024 if runq else meta["ctx"])
+    m.set_prefill(prefill)
+    prompt = meta["prompt"]
+    whole = list(m.generate(prompt, 16)["ids"])
+    first = list(m.generate(prompt, 6)["ids"])
+    rest = list(m.continue_at(len(prompt), first, 11)["ids"])
+    # first: ids drawn at positions n-1 .. n+4; fed back at n .. n+5, the draws continue from position n+5
+    assert first == whole[:6] and rest[:10] == whole[6:]
+    stop = whole[9]
+    cut = list(m.continue_at(len(prompt), first, 11, stop_id=stop)["ids"])
+    m.close()
+    assert cut == rest[:rest.index(stop)]
+
+
 def test_positions_beyond_context_are_rejected(capfd):
     m = pkg().Model(os.path.join(GOLDEN, "tiny.qwb"), 16)
     with pytest.raises(RuntimeError):
@@ -259,7 +280,9 @@ TEXT = json.load(open(os.path.join(GOLDEN, "text_ref.json")))
 def test_host_programs_text_prompts_match_reference(name, tmp_path):
     """text prompts through the hosts' tokenizers (Qwen chat template or raw, runq's BOS + dummy prefix), the
     device loop, and the generated tokens printed as text: stdout byte for byte against the reference programs
-    run with the same synthetic models and tokenizers (tests/golden/make_tokenizers.py)"""
+    run with the same synthetic models and tokenizers (tests/golden/make_tokenizers.py).  The runq chat runs
+    read their turns from stdin and continue one KV cache across turns (llm_continue), with the reference's
+    coin drawn at every position of a sampled chat."""
     run = TEXT[name]
     qwb = run["format"] == "qwb"
     exe = os.path.join(PKG_DIR, "host", "qwen_hip" if qwb else "runq_hip")
@@ -267,6 +290,7 @@ def test_host_programs_text_prompts_match_reference(name, tmp_path):
         pytest.skip(f"{exe} not built")
     model = synth(run["format"], str(tmp_path / f"m.{run['format']}"), *run["synth"])
     tok = os.path.join(GOLDEN, "qwen_tok_synth.bin" if qwb else "llama_tok_synth.bin")
-    r = subprocess.run([exe, model, *run["args"], "-z", tok], capture_output=True, timeout=120)
+    r = subprocess.run([exe, model, *run["args"], "-z", tok], capture_output=True, timeout=120,
+                       input=run.get("stdin", "").encode())
     assert r.returncode == 0, r.stderr.decode(errors="replace")
     assert r.stdout == bytes.fromhex(run["stdout_hex"])
