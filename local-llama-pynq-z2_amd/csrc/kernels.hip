@@ -836,16 +836,37 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
 // ------------------------------------------------------------------------------------------------------
 // embedding row (qwen.c:498-501, runq.c:490-492) and the step's position/token bookkeeping
 
-// argmax over the head kernel's per-block partials: larger value wins, equal values keep the lower row
-__device__ __forceinline__ void block_argmax(const float *pv, const int *pi, int np, float *sv, int *si, float *v_out,
-                                             int *i_out) {
+// The head kernel's per-block argmax partials, read by a whole block: the first STEP_PV per thread as one
+// round of loads (clamped indices), issued before anything they do not depend on is waited for.
+#define STEP_THREADS 1024
+#define STEP_PV 4
+struct Partials {
+    float v[STEP_PV];
+    int i[STEP_PV];
+};
+__device__ __forceinline__ Partials load_partials(const float *pv, const int *pi, int np) {
+    Partials p;
+#pragma unroll
+    for (int k = 0; k < STEP_PV; k++) {
+        const int j = min((int)threadIdx.x + k * (int)blockDim.x, np - 1);
+        p.v[k] = pv[j];
+        p.i[k] = pi[j];
+    }
+    return p;
+}
+
+// argmax over the partials: larger value wins, equal values keep the lower row
+__device__ __forceinline__ void block_argmax(const Partials &p, const float *pv, const int *pi, int np, float *sv,
+                                             int *si, float *v_out, int *i_out) {
     float v = -INFINITY;
     int i = 0x7fffffff;
-    for (int k = threadIdx.x; k < np; k += blockDim.x) {
-        const float x = pv[k];
-        const int xi = pi[k];
+    auto take = [&](float x, int xi) {
         if (x > v || (x == v && xi < i)) { v = x; i = xi; }
-    }
+    };
+#pragma unroll
+    for (int k = 0; k < STEP_PV; k++)
+        if ((int)threadIdx.x + k * (int)blockDim.x < np) take(p.v[k], p.i[k]);
+    for (int k = threadIdx.x + STEP_PV * blockDim.x; k < np; k += blockDim.x) take(pv[k], pi[k]);
     for (int off = 1; off < WAVE; off <<= 1) {
         float ov = __shfl_xor(v, off);
         int oi = __shfl_xor(i, off);
@@ -865,32 +886,40 @@ __device__ __forceinline__ void block_argmax(const float *pv, const int *pi, int
 
 // Start of a step.  Generate mode: finish the previous step's argmax (qwen.c:591-598, head_ids map
 // qwen.c:683), advance the position and take the prompt token or the argmax (prompt forcing,
-// qwen.c:677-683).  Then the embedding row of the token (qwen.c:498-501, runq.c:490-492).
-__global__ void __launch_bounds__(256) k_step_start(EmbedArgs a) {
-    __shared__ float sv[256 / WAVE];
-    __shared__ int si[256 / WAVE];
+// qwen.c:677-683).  Then the embedding row of the token (qwen.c:498-501, runq.c:490-492).  The dependent
+// reads form a short chain: control block (with the partials already in flight), head_ids and the prompt
+// token together, then the embedding row in one round.
+__global__ void __launch_bounds__(STEP_THREADS) k_step_start(EmbedArgs a) {
+    __shared__ float sv[STEP_THREADS / WAVE];
+    __shared__ int si[STEP_THREADS / WAVE];
     __shared__ int tok_s;
     __shared__ float bv;
-    __shared__ int bi, s_mode, s_prev;
+    __shared__ int bi, s_mode, s_prev, s_tok, s_np;
     StepCtrl *c = a.ctrl;
+    const Partials part = load_partials(a.pv, a.pi, a.np);
     // one read of the control block for the whole block, before thread 0 advances it below
     if (threadIdx.x == 0) {
         s_mode = c->mode;
         s_prev = c->pos;
+        s_tok = c->token;
+        s_np = c->n_prompt;
     }
     __syncthreads();
     const int mode = s_mode, prev = s_prev;
-    if (mode == 1 && prev >= 0) block_argmax(a.pv, a.pi, a.np, sv, si, &bv, &bi);
+    if (mode == 1 && prev >= 0) block_argmax(part, a.pv, a.pi, a.np, sv, si, &bv, &bi);
     if (threadIdx.x == 0) {
-        int pos = prev, token = c->token;
+        int pos = prev, token = s_tok;
         if (mode == 1) {
+            pos = prev + 1;
+            const int forced = pos < s_np ? a.prompt[pos] : 0;
             if (prev >= 0) {
                 const int next = a.head_ids ? a.head_ids[bi] : bi;
                 c->next_token = next;
                 if (a.gen) a.gen[prev] = next;
+                token = pos < s_np ? forced : next;
+            } else {
+                token = pos < s_np ? forced : c->next_token;
             }
-            pos = prev + 1;
-            token = pos < c->n_prompt ? a.prompt[pos] : c->next_token;
             c->pos = pos;
             c->token = token;
         }
@@ -898,28 +927,43 @@ __global__ void __launch_bounds__(256) k_step_start(EmbedArgs a) {
         tok_s = token;
     }
     __syncthreads();
-    const int token = tok_s, ngr = a.dim / a.gs;
-    const int8_t *er = a.emb_q + (size_t)token * a.dim;
-    for (int i = threadIdx.x; i < a.dim; i += blockDim.x) {
-        const int g = i / a.gs;
-        const float sc = a.sf32 ? ((const float *)a.emb_s)[(size_t)token * ngr + g]
-                                : f16_bits_to_f32(((const uint16_t *)a.emb_s)[(size_t)token * ngr + g]);
-        a.x[i] = (float)er[i] * sc;
+    const int token = tok_s, ngr = a.dim / a.gs, nt = blockDim.x;
+    const int8_t *__restrict__ er = a.emb_q + (size_t)token * a.dim;
+    float *__restrict__ x = a.x;
+    auto scale = [&](int g) {
+        return a.sf32 ? ((const float *)a.emb_s)[(size_t)token * ngr + g]
+                      : f16_bits_to_f32(((const uint16_t *)a.emb_s)[(size_t)token * ngr + g]);
+    };
+    int8_t q[STEP_PV];
+    float sc[STEP_PV];
+#pragma unroll
+    for (int k = 0; k < STEP_PV; k++) {
+        const int e = min((int)threadIdx.x + k * nt, a.dim - 1);
+        q[k] = er[e];
+        sc[k] = scale(e / a.gs);
     }
+#pragma unroll
+    for (int k = 0; k < STEP_PV; k++) {
+        const int e = threadIdx.x + k * nt;
+        if (e < a.dim) x[e] = (float)q[k] * sc[k];
+    }
+    for (int e = threadIdx.x + STEP_PV * nt; e < a.dim; e += nt) x[e] = (float)er[e] * scale(e / a.gs);
 }
 
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_step_start, dim3(1), dim3(256), 0, st, a);
+    if (a.np < 1 || a.dim < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_step_start, dim3(1), dim3(STEP_THREADS), 0, st, a);
     return hipGetLastError();
 }
 
 // final argmax of a step over the head kernel's partials (qwen.c:591-598) and the head_ids map (qwen.c:683)
-__global__ void __launch_bounds__(256) k_argmax(ArgmaxArgs a) {
-    __shared__ float sv[256 / WAVE];
-    __shared__ int si[256 / WAVE];
+__global__ void __launch_bounds__(STEP_THREADS) k_argmax(ArgmaxArgs a) {
+    __shared__ float sv[STEP_THREADS / WAVE];
+    __shared__ int si[STEP_THREADS / WAVE];
     __shared__ float bv;
     __shared__ int bi;
-    block_argmax(a.pv, a.pi, a.np, sv, si, &bv, &bi);
+    const Partials part = load_partials(a.pv, a.pi, a.np);
+    block_argmax(part, a.pv, a.pi, a.np, sv, si, &bv, &bi);
     if (threadIdx.x == 0) {
         const int next = a.head_ids ? a.head_ids[bi] : bi;
         a.ctrl->next_token = next;
@@ -928,7 +972,8 @@ __global__ void __launch_bounds__(256) k_argmax(ArgmaxArgs a) {
 }
 
 hipError_t launch_argmax(const ArgmaxArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(256), 0, st, a);
+    if (a.np < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(STEP_THREADS), 0, st, a);
     return hipGetLastError();
 }
 
