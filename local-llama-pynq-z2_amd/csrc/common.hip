@@ -58,6 +58,14 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
         }
         s.grid = iters > resident ? resident : iters;
     } else {
+        // latency shape: when the iterations outnumber the CUs, a CU would run two blocks one after the other
+        // in time; more row-blocks per iteration (more waves per block) keep it at one block per CU (a wider
+        // rule that also regrouped the streaming shapes' blocks measured slower)
+        while (iters > cus && epi != EPI_SWIGLU && (s.kw * s.nb * 2) <= 16 &&
+               !(s.ord && (size_t)s.nb * 2 * T.rb * (T.ng + 1) * 4 > 65536)) {
+            s.nb *= 2;
+            iters = (T.nblocks + s.nb - 1) / s.nb;
+        }
         s.grid = iters;
     }
     if (s.grid < 1) s.grid = 1;
