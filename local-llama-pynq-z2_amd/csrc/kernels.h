@@ -46,6 +46,7 @@ struct GemvArgs {
     // iterations per block (it_base + (block < it_rem))
     int nb_log2, rb_log2, n_it, kw_base, kw_rem, it_base, it_rem;
     int qflavor;            // activation quantization flavour (QF_QWEN / QF_RUNQ)
+    int nt;                 // 1: non-temporal weight loads (the step's weights stream past the caches)
     const StepCtrl *ctrl;
     // PRO_XQ
     const int8_t *xq;

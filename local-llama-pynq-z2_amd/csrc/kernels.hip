@@ -90,7 +90,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const TiledMat &W)
                                             0x00020000);
 }
 
-template <int WB, int GSZ, int SF32>
+// Cache policy of the weight loads (the buffer load's cache-policy operand): 0, or 2 = non-temporal (`nt`).
+// GemvArgs::nt selects non-temporal loads when a decode step streams more weights than the MALL keeps.
+template <int WB, int GSZ, int SF32, int POLICY>
 __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, uint32_t rb_off, uint32_t rec_bytes, int nchunks,
                                            int c0, int kw, int lane,
                                            uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
@@ -103,11 +105,11 @@ __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, uint32_t r
         const uint32_t soff = rb_off + (uint32_t)min(c0 + u * kw, nchunks - 1) * rec_bytes;
 #pragma unroll
         for (int p = 0; p < F::PIECES; p++) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + p * 1024, soff, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + p * 1024, soff, POLICY);
             wv[u][p] = *(const uint4 *)&v;
         }
-        if constexpr (SF32) sr[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 64 * F::SB + lane * 4, soff, 0);
-        else sr[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 64 * F::SB + lane * 2, soff, 0);
+        if constexpr (SF32) sr[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 64 * F::SB + lane * 4, soff, POLICY);
+        else sr[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 64 * F::SB + lane * 2, soff, POLICY);
     }
 }
 
@@ -192,7 +194,7 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // Slices of attention partials one merge pass loads per thread.
 #define MERGE_KB 8
 
-template <int WB, int GSZ, int SF32, int PRO, int EPI, int D>
+template <int WB, int GSZ, int SF32, int PRO, int EPI, int D, int NT>
 __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     using F = Fmt<WB, GSZ, SF32>;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -272,7 +274,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     const uint32_t rec = (uint32_t)W.rec, rb_bytes = (uint32_t)W.nchunks * rec;
     auto issue = [&](uint4 (&w)[F::UNROLL][F::PIECES], uint32_t (&sr)[F::UNROLL]) {
         const int b = min(iss_it * a.nb + my_nb, W.nblocks - 1);
-        load_batch<WB, GSZ, SF32>(wrs, (uint32_t)b * rb_bytes, rec, W.nchunks, my_kw + iss_bi * F::UNROLL * a.kw, a.kw,
+        load_batch<WB, GSZ, SF32, NT ? 2 : 0>(wrs, (uint32_t)b * rb_bytes, rec, W.nchunks, my_kw + iss_bi * F::UNROLL * a.kw, a.kw,
                                   lane, w, sr);
         if constexpr (EPI == EPI_RESID)
             if (iss_bi == 0 && iss_it != it0) pre_x_next = a.out[min(iss_it * rows_it + tid, W.rows - 1)];
@@ -602,8 +604,13 @@ template <int WB, int GSZ, int SF32, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
     const int threads = a.kw * a.nb * WAVE;
     const size_t lds = gemv_lds_bytes(a, PRO, EPI, threads);
-    if (a.depth == 4) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4>), dim3(grid), dim3(threads), lds, st, a);
-    else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2>), dim3(grid), dim3(threads), lds, st, a);
+    if (a.depth == 4) {
+        if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4, 1>), dim3(grid), dim3(threads), lds, st, a);
+        else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4, 0>), dim3(grid), dim3(threads), lds, st, a);
+    } else {
+        if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 1>), dim3(grid), dim3(threads), lds, st, a);
+        else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 0>), dim3(grid), dim3(threads), lds, st, a);
+    }
     return hipGetLastError();
 }
 

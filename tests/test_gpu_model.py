@@ -149,6 +149,23 @@ def test_decode_attention_at_long_context(tmp_path, shape):
     assert np.median([rel_err(a, b) for a, b in zip(got[0], got[1])]) < 1e-5
 
 
+@pytest.mark.parametrize("name,ctx", [("qwb", 64), ("bin", 0)])
+def test_weight_load_policy_leaves_results_bitwise_equal(monkeypatch, name, ctx):
+    """non-temporal weight loads (LLM_WEIGHTS_NT=1, the policy of models whose step streams more than the
+    MALL keeps) change only the cache policy: logits and ids bitwise equal to the default loads"""
+    meta = META[name]
+    max_new = meta["n"] if name == "qwb" else meta["steps"] - len(meta["prompt"]) + 1
+    runs = []
+    for nt in ("0", "1"):
+        monkeypatch.setenv("LLM_WEIGHTS_NT", nt)
+        m = pkg().Model(os.path.join(GOLDEN, f"tiny.{name}"), ctx or 1024)
+        m.set_prefill(False)
+        runs.append(m.generate(meta["prompt"], max_new, logits=True))
+        m.close()
+    assert list(runs[0]["ids"]) == list(runs[1]["ids"]) == meta["ids"]
+    assert np.array_equal(np.asarray(runs[0]["logits"]), np.asarray(runs[1]["logits"]))
+
+
 def test_decode_replay_and_profile_run():
     m = pkg().Model(os.path.join(GOLDEN, "tiny.qwb"), 64)
     m.generate(META["qwb"]["prompt"], 4)
