@@ -147,10 +147,11 @@ def greedy_parity(cfg, path, prompt, n_new, ids_gpu, logits_gpu):
     return out
 
 
-# HIP kernel of each step kernel kind (.qwb models: int4 layers, int8 head), as rocprofv3 names them
-KERNEL_SYMBOL = {"qkv_gemv": "k_gemv<4, 32, 0, 1, 2>", "o_gemv": "k_gemv<4, 32, 0, 2, 1>",
-                 "gateup_gemv": "k_gemv<4, 32, 0, 1, 3>", "down_gemv": "k_gemv<4, 32, 0, 0, 1>",
-                 "head_gemv": "k_gemv<8, 32, 0, 1, 4>", "attention": "k_attention", "step_start": "k_step_start"}
+# HIP kernel of each step kernel kind (.qwb models: int4 layers, int8 head), as the start of the name rocprofv3
+# gives it (the template arguments after these, stream depth and load policy, vary)
+KERNEL_SYMBOL = {"qkv_gemv": "k_gemv<4, 32, 0, 1, 2,", "o_gemv": "k_gemv<4, 32, 0, 2, 1,",
+                 "gateup_gemv": "k_gemv<4, 32, 0, 1, 3,", "down_gemv": "k_gemv<4, 32, 0, 0, 1,",
+                 "head_gemv": "k_gemv<8, 32, 0, 1, 4,", "attention": "k_attention", "step_start": "k_step_start"}
 CALIB_BYTES = 1 << 30  # the plain device copy that calibrates the byte counters (larger than any load copy)
 
 
