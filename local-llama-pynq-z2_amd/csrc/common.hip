@@ -58,9 +58,9 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
         }
         s.grid = iters > resident ? resident : iters;
     } else {
-        // latency shape: when the iterations outnumber the CUs, a CU would run two blocks one after the other
-        // in time; more row-blocks per iteration (more waves per block) keep it at one block per CU (a wider
-        // rule that also regrouped the streaming shapes' blocks measured slower)
+        // latency shape: when the iterations outnumber the CUs, some CUs hold two blocks and finish last;
+        // more row-blocks per iteration (more waves per block) keep it at one block per CU (a wider rule that
+        // also regrouped the streaming shapes' blocks measured slower)
         while (iters > cus && epi != EPI_SWIGLU && (s.kw * s.nb * 2) <= 16 &&
                !(s.ord && (size_t)s.nb * 2 * T.rb * (T.ng + 1) * 4 > 65536)) {
             s.nb *= 2;

@@ -194,6 +194,8 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 // Slices of attention partials one merge pass loads per thread.
 #define MERGE_KB 8
 
+// The decode GEMV.  WB/GSZ/SF32: weight format; PRO/EPI: prologue and epilogue; D: weight batches in flight per
+// wave; NT: non-temporal weight loads (GemvArgs::nt).
 template <int WB, int GSZ, int SF32, int PRO, int EPI, int D, int NT>
 __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     using F = Fmt<WB, GSZ, SF32>;
