@@ -257,7 +257,7 @@ def main():
     ap.add_argument("--traffic-from", default=None, help="directory with the FETCH_SIZE/WRITE_SIZE passes")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus})",
+        print(f"bench.py runs on one GPU: the decode path has no multi-GPU form (asked for --gpus {a.gpus})",
               file=sys.stderr)
         sys.exit(2)
     cfg = CONFIGS[a.config]
