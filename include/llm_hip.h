@@ -9,8 +9,13 @@
  *
  * Numerics follow the reference: int8 group quantization of activations (qwen.c:354-364 or runq.c:244-270,
  * bit-exact for the same input), exact int32 group sums, the per-group product ((float)ival * ws) * xs,
- * RoPE tables computed on the host with the reference's own libm calls.  Sums over groups, RMSNorm and
- * softmax reductions run in parallel trees, so layer outputs match the reference within fp32 rounding.
+ * RoPE tables computed on the host with the reference's own libm calls.  Two modes (llm_set_strict):
+ *   fast (default for .qwb): sums over groups, RMSNorm and softmax reductions run in parallel trees, so each
+ *     layer output matches the reference within fp32 rounding (an int8 re-quantization that lands on the
+ *     other side of a rounding boundary then moves deeper layers by more; see llm_set_strict);
+ *   strict (LLM_STRICT=1 at llm_open, or llm_set_strict): every float operation in the reference's order
+ *     and the reference libm's expf, so logits and token streams are bitwise those of qwen.c / runq.c
+ *     built with strict IEEE flags.  llama2.c .bin GEMVs always sum their groups in order.
  * Errors: -1 (or NULL) with a message on stderr, the reference's convention (matvec_fpga.h:15). */
 #pragma once
 #include <stddef.h>
@@ -105,6 +110,17 @@ int llm_prefill(llm_model *m, const int *ids, int n, float *logits);
  * position.  The --logits history (llm_generate with `logits`) always uses the per-position steps. */
 int llm_set_prefill(llm_model *m, int on);
 
+/* Reference-order ("strict") mode on or off; no counterpart in the reference, whose CPU loops are this order
+ * (qwen.c:337-352 rmsnorm and softmax, 407-457 matmul_cpu, 526-546 attention, 558-562 SiLU; runq.c:394-428,
+ * 429-458, 530-568, 589-596).  On: GEMV group products added per row in group order, RMSNorm's sum of squares
+ * as one running sum, attention per head as scores -> max -> expf -> running sum -> divide -> position-ordered
+ * weighted sum of V, and expf evaluated as the reference's glibc computes it.  Applies to decode steps and
+ * to the batched prefill (whose GEMM keeps the group order in both modes).  Slower than the fast mode (the
+ * running sums are single dependency chains).  The step graphs are re-captured on the next call.
+ * llm_get_strict returns 1, 0, or -1 for a NULL model.  Returns 0 or -1. */
+int llm_set_strict(llm_model *m, int on);
+int llm_get_strict(const llm_model *m);
+
 /* Sampling in llm_generate (the reference's sampler, qwen.c:578-654 / runq.c:830-967, which its hosts run on
  * the CPU per token): with temperature > 0 every generated token is drawn on the device inside the step
  * graph (logits / temperature, softmax, top-p when 0 < topp < 1 else the plain cdf walk, xorshift64* coin
@@ -133,6 +149,10 @@ int mvh_sample(const float *logits, int n, int count, float temperature, float t
  * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d] */
 int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
                      int bits, int gs, int rb, float *y);
+/* expf as the reference's C library evaluates it (the strict mode's softmax and SiLU), over n floats: on the
+ * device (n <= 2^26), and the same restatement compiled for the host CPU (no GPU involved) */
+int mvh_ref_expf(const float *x, int n, float *y);
+int mvh_ref_expf_host(const float *x, int n, float *y);
 /* device state after the last llm_forward/llm_generate step: 0 = residual stream x (dim floats, after the
  * final rmsnorm like qwen.c:569), 1 = key cache of layer `layer` (ctx * kv_dim), 2 = value cache */
 int llm_read_state(llm_model *m, int which, int layer, float *dst, size_t count);

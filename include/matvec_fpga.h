@@ -11,16 +11,20 @@
  *     weights once at load (qwen.c:162-163, runq.c:167-168) and never again,
  *   - the activation ranges (xq, xs) are copied host->device on every call,
  *   - the output range is copied device->host before the call returns.
- * Calls are synchronous, like the reference's (matvec_fpga.cpp:193-207).  State is process-global and not
- * thread-safe, like the reference's (matvec_fpga.cpp:87-93).
+ * Calls are synchronous, like the reference's (run_kernel polls ap_done, matvec_fpga.cpp:156-170).  State is
+ * process-global and not thread-safe, like the reference's (its file-scope state, matvec_fpga.cpp:50-56).
  *
  * Differences from the reference contract, all of them relaxations:
- *   - n may be up to MATVEC_HIP_MAX_N (the reference stops at 8192, matvec_fpga.cpp:70), so the Qwen2-7B
- *     down projection (n = 18944) runs;
+ *   - n may be up to MATVEC_HIP_MAX_N (the reference stops at MAX_N 8192, matvec_fpga.cpp:33, 178, 212), so
+ *     the Qwen2-7B down projection (n = 18944) runs;
  *   - one library exports both fpga_matvec (runq flavour) and fpga_matvec4 (qwen flavour); the reference
- *     builds one or the other (matvec_fpga.cpp:209, 236).
- * Env: FPGA_MEMIDX = HIP device ordinal (the reference's bank index, matvec_fpga.cpp:120-128);
- *      FPGA_TIMEOUT_MS = completion wait limit, default 5000 (the reference's TIMEOUT_S, matvec_fpga.cpp:71). */
+ *     builds one or the other (#ifndef MATVEC4, matvec_fpga.cpp:172-233);
+ *   - fpga_matvec, like the reference's, takes any address; ranges that the kernel cannot read or write as
+ *     aligned vectors are staged through aligned device buffers inside the call.
+ * Env: FPGA_MEMIDX = HIP device ordinal (the reference's bank index, matvec_fpga.cpp:83-91);
+ *      FPGA_TIMEOUT_MS = completion wait limit, default 5000 (the reference's TIMEOUT_S, matvec_fpga.cpp:34);
+ *      LLM_STRICT = 1: fpga_matvec4 adds each row's groups in order, as qwen.c's matmul_cpu does
+ *      (qwen.c:452-455), so a -DFPGA qwen.c reproduces the CPU build's logits bit for bit. */
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -54,8 +58,9 @@ int fpga_matvec(uint64_t wq, uint64_t ws, uint64_t xq, uint64_t xs, uint64_t out
  * with fp16 scales per group of 32, int8 activations with fp32 scales:
  *   out[i] = sum_g ((float)(group int sum) * f16(ws[i*n/32 + g])) * xs[g]
  * Group sums are exact int32; the fp32 sum over groups is taken in a tree, within the reference testbench's
- * bound |out - exact| <= 1e-5 * sum_g |term_g| (hls4/matvec4_tb.cpp:1-7, 19).  Every address must be 64-byte
- * aligned and n % 32 == 0 (matvec_fpga.cpp:249).  Returns 0, or -1 with a message on stderr. */
+ * bound |out - exact| <= 1e-5 * sum_g |term_g| (hls4/matvec4_tb.cpp:1-7, 19, 67-79), or in group order with
+ * LLM_STRICT=1.  Every address must be 64-byte aligned and n % 32 == 0, as the reference requires
+ * (matvec_fpga.cpp:212-216).  Returns 0, or -1 with a message on stderr. */
 int fpga_matvec4(uint64_t w, uint64_t ws, uint64_t xq, uint64_t xs, uint64_t out, int n, int d, int wbits);
 
 /* matvec_fpga.h:32-33.  Free every buffer and the device state.  Safe to call more than once. */

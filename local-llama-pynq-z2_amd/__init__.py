@@ -84,6 +84,10 @@ def lib():
     L.llm_set_sampler.argtypes = [vp, C.c_float, C.c_float, C.c_ulonglong]
     L.llm_sampler_state.argtypes = [vp, C.POINTER(C.c_ulonglong)]
     L.mvh_sample.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
+    L.mvh_ref_expf.argtypes = [vp, i32, vp]
+    L.mvh_ref_expf_host.argtypes = [vp, i32, vp]
+    L.llm_set_strict.argtypes = [vp, i32]
+    L.llm_get_strict.argtypes = [vp]
     _lib = L
     return L
 
@@ -136,6 +140,17 @@ def sample(logits, temperature, topp, seed):
     if lib().mvh_sample(_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)) != 0:
         raise RuntimeError("mvh_sample failed")
     return rows, st.value
+
+
+def ref_expf(x, host=False):
+    """expf as the reference's C library evaluates it (the strict mode's softmax and SiLU): on the device, or
+    the same restatement compiled for the host CPU with host=True"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    fn = lib().mvh_ref_expf_host if host else lib().mvh_ref_expf
+    if fn(_ptr(x), x.size, _ptr(y)) != 0:
+        raise RuntimeError("mvh_ref_expf failed")
+    return y
 
 
 # ---- drop-in driver API -----------------------------------------------------------------------------------
@@ -270,6 +285,15 @@ class Model:
         if self.L.llm_sampler_state(self.h, C.byref(st)) != 0:
             raise RuntimeError("llm_sampler_state failed")
         return st.value
+
+    def set_strict(self, on):
+        """reference-order mode: logits bitwise those of the reference's strict-IEEE build (llm_set_strict)"""
+        if self.L.llm_set_strict(self.h, 1 if on else 0) != 0:
+            raise RuntimeError("llm_set_strict failed")
+
+    @property
+    def strict(self):
+        return self.L.llm_get_strict(self.h) == 1
 
     def set_prefill(self, on):
         """whether generate() runs the prompt as one batched prefill (default) or one step per position"""

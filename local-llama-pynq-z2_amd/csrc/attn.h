@@ -7,6 +7,7 @@
 #pragma once
 #include "device.h"
 #include "kernels.h"
+#include "ref_expf.h"
 
 #ifndef KERNEL_MARK
 #define KERNEL_MARK(k)
@@ -131,4 +132,82 @@ __device__ __forceinline__ void attn_range(const float *q, const float *kc, cons
     }
     *ml_max = sm_;
     *ml_sum = sl;
+}
+
+// ------------------------------------------------------------------------------------------------------
+// Reference-order attention (the strict mode): one query head over positions 0 .. P-1 with every float
+// operation of qwen.c:526-546 / runq.c:530-568 in the reference's order, so the result is bitwise the
+// reference's:
+//   score_t = (sum over i in order of q[i] * k_t[i]) / sqrtf(hs);  max over t (exact in any order);
+//   e_t = expf(score_t - max) (ref_expf: the reference libm's expf);  sum = e_0 + e_1 + ... in position order;
+//   a_t = e_t / sum;  out[e] = ((0 + a_0 v_0[e]) + a_1 v_1[e]) + ... in position order.
+// The scores and products run in parallel; the two running sums are single chains, as in the reference.
+// Block-wide (barriers inside); every thread of the block calls it.  sm: attn_strict_lds_floats floats.
+
+__host__ __device__ inline size_t attn_strict_lds_floats(int hs, int P, int threads) {
+    return (size_t)hs + (size_t)P + (size_t)threads / WAVE + 4;
+}
+
+__device__ __forceinline__ void attn_strict_head(const float *q, const float *kc, const float *vc, int kv_dim,
+                                                 int koff, int hs, int P, float *sm, float *out) {
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & (WAVE - 1), wave = tid / WAVE, nw = nt / WAVE;
+    float *sq = sm, *sc = sm + hs, *sred = sc + P;
+    for (int i = tid; i < hs; i += nt) sq[i] = q[i];
+    __syncthreads();
+    const float rs = sqrtf((float)hs);
+    float mx = -INFINITY;
+    for (int t = tid; t < P; t += nt) {
+        const f32x4 *k4 = (const f32x4 *)(kc + (size_t)t * kv_dim + koff);
+        float d = 0.0f;
+        for (int i4 = 0; i4 < hs / 4; i4++) {
+            const f32x4 kk = k4[i4];
+            d += sq[4 * i4] * kk.x;
+            d += sq[4 * i4 + 1] * kk.y;
+            d += sq[4 * i4 + 2] * kk.z;
+            d += sq[4 * i4 + 3] * kk.w;
+        }
+        const float s = d / rs;
+        sc[t] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) sred[wave] = mx;
+    __syncthreads();
+    for (int w = 0; w < nw; w++) mx = fmaxf(mx, sred[w]);
+    for (int t = tid; t < P; t += nt) sc[t] = ref_expf(sc[t] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        int t = 0;
+        for (; t + 8 <= P; t += 8) {
+            float e[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) e[u] = sc[t + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) sum += e[u];
+        }
+        for (; t < P; t++) sum += sc[t];
+        sred[nw] = sum;
+    }
+    __syncthreads();
+    const float sum = sred[nw];
+    for (int t = tid; t < P; t += nt) sc[t] = sc[t] / sum;
+    __syncthreads();
+    for (int e = tid; e < hs; e += nt) {
+        const float *v = vc + koff + e;
+        float acc = 0.0f;
+        int t = 0;
+        for (; t + 8 <= P; t += 8) {
+            float vv[8], aa[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                vv[u] = v[(size_t)(t + u) * kv_dim];
+                aa[u] = sc[t + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc += aa[u] * vv[u];
+        }
+        for (; t < P; t++) acc += sc[t] * v[(size_t)t * kv_dim];
+        out[e] = acc;
+    }
 }

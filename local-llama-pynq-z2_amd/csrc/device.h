@@ -101,6 +101,24 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
     return t;
 }
 
+// The reference's RMSNorm sum (qwen.c:337-339, runq.c:394-398): ss = x[0]^2 + x[1]^2 + ... as one running
+// fp32 sum in element order (one thread; v 16-byte aligned, n a multiple of 8).
+__device__ __forceinline__ float seq_sum_squares(const float *v, int n) {
+    float ss = 0.0f;
+    for (int j = 0; j < n; j += 8) {
+        const float4 a = *(const float4 *)(v + j), b = *(const float4 *)(v + j + 4);
+        ss += a.x * a.x;
+        ss += a.y * a.y;
+        ss += a.z * a.z;
+        ss += a.w * a.w;
+        ss += b.x * b.x;
+        ss += b.y * b.y;
+        ss += b.z * b.z;
+        ss += b.w * b.w;
+    }
+    return ss;
+}
+
 // Quantize n floats held in LDS (`v`, 16-byte aligned) into int8 `q` (4-byte aligned) and fp32 scales `s`
 // (LDS or global), groups of gs (32 or 64; n a multiple of gs), by the whole block.  Each lane takes 4
 // consecutive values, so a group is gs/4 = 8 or 16 lanes of one DPP row and its max is max8 / max16.

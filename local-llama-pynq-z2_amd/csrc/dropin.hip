@@ -1,11 +1,13 @@
 // The reference's board driver API (driver/matvec_fpga.h) on one MI355X.  See include/matvec_fpga.h for
 // the contract; this file keeps the reference driver's behaviour where it is observable: idempotent open
-// (matvec_fpga.cpp:154-161), the alloc / alloc_try pair with the failure reason kept for the next alloc
-// (163-191), argument validation with one stderr line and -1 (209-219, 244-253), a completion time limit
-// (193-207) and a close that frees everything (272-280).
+// (matvec_fpga.cpp:117-124), the alloc / alloc_try pair with the failure reason kept for the next alloc
+// (126-154), argument validation with one stderr line and -1 (178-182, 212-216), a completion time limit
+// (156-170, 192-196, 226-230) and a close that frees everything (235-243).
 #include <algorithm>
+#include <map>
 #include <string.h>
 #include <time.h>
+#include <tuple>
 #include <vector>
 
 #include "../../include/matvec_fpga.h"
@@ -19,12 +21,13 @@ struct Buf {
 };
 
 struct Weight { // one matrix, uploaded and repacked at its first use
-    uint64_t w, ws;
-    int n, d, code; // code: wbits | gs << 8 | sf32 << 16
     uint8_t *tiled;
     TiledMat T;
     GemvShape shape;
 };
+// a matrix is identified by its planes' device addresses, its shape and its format code
+// (wbits | gs << 8 | sf32 << 16 | ordered << 24)
+typedef std::tuple<uint64_t, uint64_t, int, int, int> WeightKey;
 
 struct State {
     bool open = false;
@@ -32,12 +35,16 @@ struct State {
     hipStream_t st = nullptr;
     long timeout_ms = 5000;
     std::vector<Buf> bufs;       // sorted by dev
-    std::vector<Weight> weights;
+    std::map<WeightKey, Weight> weights; // node-based: a Weight's address stays valid as others are added
     size_t total = 0;
     char last_err[256] = "";
     uint8_t *stage = nullptr;    // int rowmap for repacks
     int8_t *xstage = nullptr;    // activations whose device address is not 16-byte aligned (the kernel reads
                                  // them as 16-byte vectors)
+    float *sstage = nullptr;     // activation scales whose device address is not 4-byte aligned
+    float *ostage = nullptr;     // outputs whose device address is not 4-byte aligned
+    size_t ostage_n = 0;
+    int strict = 0;              // LLM_STRICT=1: fpga_matvec4 adds a row's groups in order (qwen.c:452-455)
     int *rowmap = nullptr;
     size_t rowmap_n = 0;
 };
@@ -71,9 +78,9 @@ int ensure_rowmap(size_t rows) {
 
 // the resident tiled copy of a weight matrix; uploads and repacks it the first time
 const Weight *weight(const char *who, uint64_t w, uint64_t ws, int n, int d, int wbits, int gs, int sf32, int ordered) {
-    const int code = wbits | gs << 8 | sf32 << 16;
-    for (const Weight &x : S.weights)
-        if (x.w == w && x.ws == ws && x.n == n && x.d == d && x.code == code) return &x;
+    const WeightKey key(w, ws, n, d, wbits | gs << 8 | sf32 << 16 | ordered << 24);
+    const auto found = S.weights.find(key);
+    if (found != S.weights.end()) return &found->second;
     const size_t wbytes = (size_t)d * n * wbits / 8, sbytes = (size_t)d * (n / gs) * (sf32 ? 4 : 2);
     const Buf *bw = find(w, wbytes), *bs = find(ws, sbytes);
     if (!bw || !bs) {
@@ -88,7 +95,6 @@ const Weight *weight(const char *who, uint64_t w, uint64_t ws, int n, int d, int
     }
     if (ensure_rowmap((size_t)d)) return nullptr;
     Weight x;
-    x.w = w; x.ws = ws; x.n = n; x.d = d; x.code = code;
     x.T = tiled_describe(d, n, gs, wbits, sf32, ordered ? 64 : 16);
     if (hipMalloc(&x.tiled, x.T.bytes) != hipSuccess) {
         fprintf(stderr, "%s: cannot allocate %zu bytes of HBM for a weight matrix\n", who, x.T.bytes);
@@ -107,8 +113,7 @@ const Weight *weight(const char *who, uint64_t w, uint64_t ws, int n, int d, int
         return nullptr;
     }
     x.shape = gemv_pick_shape(x.T, PRO_XQ, EPI_STORE, ordered, hip_cu_count(S.device));
-    S.weights.push_back(x);
-    return &S.weights.back();
+    return &S.weights.emplace(key, x).first->second;
 }
 
 int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out, int n, int d, int gs) {
@@ -122,8 +127,25 @@ int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out
         if (!S.xstage) HIP_OR_FAIL(who, hipMalloc(&S.xstage, MATVEC_HIP_MAX_N));
         xdev = S.xstage;
     }
+    // the kernel reads the scales and writes the outputs as floats: ranges at addresses that are not 4-byte
+    // aligned go through aligned staging buffers (the reference's driver takes any address for fpga_matvec)
+    float *sdev = (float *)xs, *odev = (float *)out;
+    if (xs & 3) {
+        if (!S.sstage) HIP_OR_FAIL(who, hipMalloc(&S.sstage, MATVEC_HIP_MAX_N / 32 * 4));
+        sdev = S.sstage;
+    }
+    if (out & 3) {
+        if ((size_t)d > S.ostage_n) {
+            if (S.ostage) hipFree(S.ostage);
+            S.ostage = nullptr;
+            S.ostage_n = 0;
+            HIP_OR_FAIL(who, hipMalloc(&S.ostage, (size_t)d * 4));
+            S.ostage_n = (size_t)d;
+        }
+        odev = S.ostage;
+    }
     HIP_OR_FAIL(who, hipMemcpyAsync(xdev, host_of(bx, xq), (size_t)n, hipMemcpyHostToDevice, S.st));
-    HIP_OR_FAIL(who, hipMemcpyAsync((void *)xs, host_of(bxs, xs), (size_t)(n / gs) * 4, hipMemcpyHostToDevice, S.st));
+    HIP_OR_FAIL(who, hipMemcpyAsync(sdev, host_of(bxs, xs), (size_t)(n / gs) * 4, hipMemcpyHostToDevice, S.st));
     GemvArgs a;
     memset(&a, 0, sizeof a);
     a.W = W->T;
@@ -132,10 +154,12 @@ int run(const char *who, const Weight *W, uint64_t xq, uint64_t xs, uint64_t out
     a.depth = W->shape.depth;
     a.ord = W->shape.ord;
     a.xq = xdev;
-    a.xs = (const float *)xs;
-    a.out = (float *)out;
+    a.xs = sdev;
+    a.out = odev;
     HIP_OR_FAIL(who, launch_gemv(W->T.wbits, W->T.gs, W->T.sf32, PRO_XQ, EPI_STORE, a, W->shape.grid, S.st));
-    HIP_OR_FAIL(who, hipMemcpyAsync(host_of(bo, out), (void *)out, (size_t)d * 4, hipMemcpyDeviceToHost, S.st));
+    if (odev != (float *)out) // keep the twin equal to the host copy
+        HIP_OR_FAIL(who, hipMemcpyAsync((void *)out, odev, (size_t)d * 4, hipMemcpyDeviceToDevice, S.st));
+    HIP_OR_FAIL(who, hipMemcpyAsync(host_of(bo, out), odev, (size_t)d * 4, hipMemcpyDeviceToHost, S.st));
     int r = stream_wait(S.st, S.timeout_ms, who);
     if (r == 1) {
         fprintf(stderr, "%s: kernel did not finish in %ld ms (n=%d d=%d)\n", who, S.timeout_ms, n, d);
@@ -168,6 +192,7 @@ int open_impl() {
         }
         S.timeout_ms = v;
     }
+    if (const char *e = getenv("LLM_STRICT")) S.strict = atoi(e) != 0;
     S.open = true;
     return 0;
 }
@@ -225,9 +250,9 @@ extern "C" int fpga_matvec(uint64_t wq, uint64_t ws, uint64_t xq, uint64_t xs, u
         fprintf(stderr, "fpga_matvec: fpga_open() not called\n");
         return -1;
     }
-    if ((gs != 32 && gs != 64) || n <= 0 || n > MATVEC_HIP_MAX_N || n % gs || d <= 0 || ((ws | xq | xs | out) & 3)) {
-        fprintf(stderr, "fpga_matvec: unsupported n=%d d=%d gs=%d (need gs 32 or 64, n %% gs == 0, n <= %d, "
-                "4-byte aligned xq, xs, ws, out)\n", n, d, gs, MATVEC_HIP_MAX_N);
+    if ((gs != 32 && gs != 64) || n <= 0 || n > MATVEC_HIP_MAX_N || n % gs || d <= 0) {
+        fprintf(stderr, "fpga_matvec: unsupported n=%d d=%d gs=%d (need gs 32 or 64, n %% gs == 0, n <= %d)\n",
+                n, d, gs, MATVEC_HIP_MAX_N);
         return -1;
     }
     hipSetDevice(S.device);
@@ -247,7 +272,7 @@ extern "C" int fpga_matvec4(uint64_t w, uint64_t ws, uint64_t xq, uint64_t xs, u
         return -1;
     }
     hipSetDevice(S.device);
-    const Weight *W = weight("fpga_matvec4", w, ws, n, d, wbits, 32, 0, 0);
+    const Weight *W = weight("fpga_matvec4", w, ws, n, d, wbits, 32, 0, S.strict);
     if (!W) return -1;
     return run("fpga_matvec4", W, xq, xs, out, n, d, 32);
 }
@@ -257,7 +282,7 @@ extern "C" void fpga_close(void) {
         hipSetDevice(S.device);
         if (S.st) hipStreamSynchronize(S.st);
     }
-    for (Weight &x : S.weights) hipFree(x.tiled);
+    for (auto &x : S.weights) hipFree(x.second.tiled);
     S.weights.clear();
     for (Buf &b : S.bufs) {
         hipHostFree(b.host);
@@ -267,8 +292,12 @@ extern "C" void fpga_close(void) {
     if (S.rowmap) hipFree(S.rowmap);
     S.rowmap = nullptr;
     S.rowmap_n = 0;
-    if (S.xstage) hipFree(S.xstage);
+    for (void *p : {(void *)S.xstage, (void *)S.sstage, (void *)S.ostage})
+        if (p) hipFree(p);
     S.xstage = nullptr;
+    S.sstage = nullptr;
+    S.ostage = nullptr;
+    S.ostage_n = 0;
     if (S.st) hipStreamDestroy(S.st);
     S.st = nullptr;
     S.total = 0;

@@ -6,6 +6,7 @@
 #include "../../include/llm_hip.h"
 #include "host_common.h"
 #include "prefill.h"
+#include "ref_expf.h"
 
 namespace {
 int hook_device(const char *who) {
@@ -189,4 +190,38 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     hipFree(dr);
     hipFree(dss);
     return rc;
+}
+
+// ref_expf (the reference libm's expf, used by the strict mode) over caller data, on the device and, with the
+// same source compiled for the host, on the CPU; the tests hold both to the C library's own expf
+__global__ void k_ref_expf(const float *x, int n, float *y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ref_expf(x[i]);
+}
+
+extern "C" int mvh_ref_expf(const float *x, int n, float *y) {
+    if (!x || !y || n <= 0 || n > (1 << 26)) {
+        fprintf(stderr, "mvh_ref_expf: bad arguments (n=%d)\n", n);
+        return -1;
+    }
+    if (hook_device("mvh_ref_expf")) return -1;
+    float *dx = nullptr, *dy = nullptr;
+    int rc = -1;
+    if (hipMalloc(&dx, (size_t)n * 4) == hipSuccess && hipMalloc(&dy, (size_t)n * 4) == hipSuccess &&
+        hipMemcpy(dx, x, (size_t)n * 4, hipMemcpyHostToDevice) == hipSuccess) {
+        hipLaunchKernelGGL(k_ref_expf, dim3((n + 255) / 256), dim3(256), 0, 0, dx, n, dy);
+        if (hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+            hipMemcpy(y, dy, (size_t)n * 4, hipMemcpyDeviceToHost) == hipSuccess)
+            rc = 0;
+    }
+    if (rc) fprintf(stderr, "mvh_ref_expf: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    hipFree(dx);
+    hipFree(dy);
+    return rc;
+}
+
+extern "C" int mvh_ref_expf_host(const float *x, int n, float *y) {
+    if (!x || !y || n < 0) return -1;
+    for (int i = 0; i < n; i++) y[i] = ref_expf_with(x[i], ref_expf_tab_host);
+    return 0;
 }

@@ -16,7 +16,7 @@
         }                                                                                            \
     } while (0)
 
-// Device ordinal from FPGA_MEMIDX (the reference's memory-bank selector, matvec_fpga.cpp:120-128), default 0.
+// Device ordinal from FPGA_MEMIDX (the reference's memory-bank selector, matvec_fpga.cpp:83-91), default 0.
 // Returns -1 with a message on a malformed value.
 static inline int hip_device_from_env(const char *who) {
     const char *e = getenv("FPGA_MEMIDX");
@@ -51,6 +51,6 @@ static inline int hip_cu_count(int dev) {
 // Row-block size for a plain matrix of d rows x n inputs (fused QKV and gate/up keep 16 for their pairing).
 int gemv_row_block(int d, int n);
 
-// Wait for the stream with a time limit (the reference's 5 s ap_done poll, matvec_fpga.cpp:193-207).
+// Wait for the stream with a time limit (the reference's 5 s ap_done poll, matvec_fpga.cpp:34, 156-170).
 // Returns 0, 1 on time-out, -1 on a HIP error (message printed).
 int stream_wait(hipStream_t st, long timeout_ms, const char *who);

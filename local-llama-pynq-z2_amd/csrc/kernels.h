@@ -47,6 +47,7 @@ struct GemvArgs {
     int nb_log2, rb_log2, n_it, kw_base, kw_rem, it_base, it_rem;
     int qflavor;            // activation quantization flavour (QF_QWEN / QF_RUNQ)
     int nt;                 // 1: non-temporal weight loads (the step's weights stream past the caches)
+    int strict;             // 1: reference order (sequential RMSNorm sum, the reference libm's expf in SiLU)
     const StepCtrl *ctrl;
     // PRO_XQ
     const int8_t *xq;
@@ -140,6 +141,9 @@ struct RepackArgs {
 hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const GemvArgs &a, int grid, hipStream_t st);
 size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st);
+// reference-order attention (one block per query head); leaves acc [n_heads][hs] and ml = (0, 1) per head,
+// i.e. the partials of a single slice that the o projection's merge passes through unchanged
+hipError_t launch_attention_strict(const AttnArgs &a, hipStream_t st);
 hipError_t launch_embed(const EmbedArgs &a, hipStream_t st);
 hipError_t launch_argmax(const ArgmaxArgs &a, hipStream_t st);
 hipError_t launch_repack(const RepackArgs &a, hipStream_t st);

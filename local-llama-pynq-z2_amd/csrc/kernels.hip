@@ -354,7 +354,18 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                 part += v.w * v.w;
             }
             KERNEL_MARK(2);
-            float ss = block_sum(part, sred);
+            float ss;
+            if (a.strict) { // one running sum in element order, as the reference's loop
+#pragma unroll
+                for (int k = 0; k < PRO_VEC; k++)
+                    if (tid + k * nt < nv) sv4[tid + k * nt] = pn[k];
+                __syncthreads();
+                if (tid == 0) sred[0] = seq_sum_squares(sv, n);
+                __syncthreads();
+                ss = sred[0];
+            } else {
+                ss = block_sum(part, sred);
+            }
             ss /= (float)n;
             ss += a.eps;
             ss = 1.0f / sqrtf(ss);
@@ -524,7 +535,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                 const int nbi = tid >> a.rb_log2, r = tid & (rb - 1);
                 if (r < hb) {
                     float g = srow[tid], u = srow[tid + hb];
-                    float sig = 1.0f / (1.0f + expf(-g));
+                    float sig = 1.0f / (1.0f + (a.strict ? ref_expf(-g) : expf(-g)));
                     g = g * sig;
                     sv[nbi * hb + r] = g * u;
                 }
@@ -818,6 +829,27 @@ __global__ void __launch_bounds__(512) k_attention_short(AttnArgs a) {
         ml[1] = l;
     }
     KERNEL_MARK(7);
+}
+
+// Reference-order decode attention: block h is query head h over positions 0 .. pos (attn_strict_head); the
+// output goes to acc[h][0..hs) with (max, sum) = (0, 1), one slice whose merge is the identity.
+__global__ void __launch_bounds__(256) k_attention_strict(AttnArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    const int pos = a.ctrl->pos, h = blockIdx.x, kv_mul = a.n_heads / a.n_kv, hs = a.hs;
+    attn_strict_head(a.q + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs, pos + 1, sm,
+                     a.acc + (size_t)h * hs);
+    if (threadIdx.x == 0) {
+        a.ml[2 * h] = 0.0f;
+        a.ml[2 * h + 1] = 1.0f;
+    }
+}
+
+hipError_t launch_attention_strict(const AttnArgs &a, hipStream_t st) {
+    const size_t lds = attn_strict_lds_floats(a.hs, a.max_pos, 256) * 4;
+    if (a.hs % 4 || ((uintptr_t)a.kc & 15) || (a.kv_dim % 4) || a.max_pos < 1 || lds > 65536 || a.n_heads % a.n_kv)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attention_strict, dim3(a.n_heads), dim3(256), lds, st, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {

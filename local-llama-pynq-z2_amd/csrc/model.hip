@@ -59,6 +59,11 @@ struct llm_model {
     // 1.634 -> 1.547 ms; the llama2.c 288/6L and 768/12L shapes (17 and 124 MB, MALL-resident) 3-6% slower
     // with it, so they keep the default policy.
     int weights_nt = 0;
+    // Reference-order mode (llm_set_strict, LLM_STRICT=1): every float operation in the reference's order, so
+    // logits are bitwise those of qwen.c / runq.c built with strict IEEE flags.  GEMV group products summed per
+    // row in group order, RMSNorm's sum of squares as one running sum, attention by attn_strict_head, and the
+    // reference libm's expf (ref_expf) in SiLU and softmax.
+    int strict = 0;
     int device = 0;
     hipStream_t st = nullptr;
     std::vector<void *> allocs;
@@ -75,6 +80,7 @@ struct llm_model {
     float *logits = nullptr, *hist = nullptr, *part_v = nullptr, *hsc = nullptr;
     int8_t *hq = nullptr;
     int *part_i = nullptr;
+    int part_cap = 0; // argmax partials allocated (the larger head grid of the two modes)
     StepCtrl *ctrl = nullptr;
     int *prompt = nullptr, *tokens = nullptr, *gen = nullptr;
     hipGraphExec_t g_plain = nullptr, g_hist = nullptr;
@@ -123,6 +129,7 @@ GemvArgs base_args(const llm_model *m, const TiledMat &T, const GemvShape &s) {
     a.nt = m->weights_nt;
     a.ctrl = m->ctrl;
     a.eps = m->info.rms_eps;
+    a.strict = m->strict;
     return a;
 }
 
@@ -278,7 +285,12 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         t.ctrl = m->ctrl;
         if (on(K_ATTN)) {
             mark(K_ATTN, kind_bytes(m, K_ATTN, pos_hint));
-            HIP_OR_FAIL("llm", launch_attention(t, m->st));
+            if (m->strict) {
+                t.splits = 1;
+                HIP_OR_FAIL("llm", launch_attention_strict(t, m->st));
+            } else {
+                HIP_OR_FAIL("llm", launch_attention(t, m->st));
+            }
             done();
         }
 
@@ -287,7 +299,7 @@ int enqueue_step(llm_model *m, bool hist, Prof *prof, int pos_hint, bool finaliz
         a.att_acc = m->att_acc;
         a.n_heads = I.n_heads;
         a.head_size = m->hs;
-        a.att_splits = m->att_splits;
+        a.att_splits = m->strict ? 1 : m->att_splits; // strict: one slice, merged as the identity
         a.out = m->x;
         if (on(K_O)) {
             mark(K_O, kind_bytes(m, K_O, pos_hint));
@@ -428,19 +440,40 @@ std::vector<int> rowmap_gateup(int hidden, int rb) { // row-block: rb/2 gate row
 
 struct Src { const uint8_t *w, *s; };
 
-int finish_setup(llm_model *m) {
-    const llm_info &I = m->info;
+// GEMV launch shapes of every matrix: group products summed in group order for runq (whose reference sums
+// them sequentially, runq.c:452-456, as its FPGA kernel's test bar demands) and in the strict mode.
+int pick_shapes(llm_model *m) {
     const int cus = hip_cu_count(m->device);
     if (!cus) return -1;
-    // per-layer shapes
+    const int ord = m->kind == 1 || m->strict;
     for (Layer &ly : m->L) {
-        const int ord = m->kind == 1;
         ly.s_qkv = gemv_pick_shape(ly.qkv, PRO_NORM, EPI_QKV, ord, cus);
         ly.s_o = gemv_pick_shape(ly.o, PRO_ATTN, EPI_RESID, ord, cus);
         ly.s_gu = gemv_pick_shape(ly.gu, PRO_NORM, EPI_SWIGLU, ord, cus);
         ly.s_down = gemv_pick_shape(ly.down, PRO_XQ, EPI_RESID, ord, cus);
     }
-    m->s_head = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, m->kind == 1, cus);
+    const GemvShape h = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, ord, cus);
+    if (m->part_cap && h.grid > m->part_cap) { // the argmax partials are sized at load for both modes
+        fprintf(stderr, "llm: internal error: head grid %d over %d partials\n", h.grid, m->part_cap);
+        return -1;
+    }
+    m->s_head = h;
+    return 0;
+}
+
+int finish_setup(llm_model *m) {
+    const llm_info &I = m->info;
+    if (const char *e = getenv("LLM_STRICT")) m->strict = atoi(e) != 0;
+    // the argmax partials are sized for the larger of the two head grids (fast and ordered)
+    int head_grid = 0;
+    for (int st = 0; st < 2; st++) {
+        const int keep = m->strict;
+        m->strict = st;
+        if (pick_shapes(m)) return -1;
+        head_grid = std::max(head_grid, m->s_head.grid);
+        m->strict = keep;
+    }
+    if (pick_shapes(m)) return -1;
     // attention slices: up to 64 per kv head, each at least ATT_SUB positions
     m->att_splits = (m->ctx + ATT_SUB - 1) / ATT_SUB;
     if (m->att_splits > 64) m->att_splits = 64;
@@ -449,12 +482,13 @@ int finish_setup(llm_model *m) {
         dalloc(m, &m->q, (size_t)I.dim * 4) ||
         dalloc(m, &m->att_ml, (size_t)I.n_heads * m->att_splits * 2 * 4) ||
         dalloc(m, &m->att_acc, (size_t)I.n_heads * m->att_splits * m->hs * 4) ||
-        dalloc(m, &m->logits, (size_t)I.n_logits * 4) || dalloc(m, &m->part_v, (size_t)m->s_head.grid * 4) ||
-        dalloc(m, &m->part_i, (size_t)m->s_head.grid * 4) || dalloc(m, &m->hq, (size_t)I.hidden_dim) ||
+        dalloc(m, &m->logits, (size_t)I.n_logits * 4) || dalloc(m, &m->part_v, (size_t)head_grid * 4) ||
+        dalloc(m, &m->part_i, (size_t)head_grid * 4) || dalloc(m, &m->hq, (size_t)I.hidden_dim) ||
         dalloc(m, &m->hsc, (size_t)I.hidden_dim / m->gs * 4) || dalloc(m, &m->ctrl, sizeof(StepCtrl)) ||
         dalloc(m, &m->prompt, (size_t)m->ctx * 4) || dalloc(m, &m->tokens, (size_t)m->ctx * 4) ||
         dalloc(m, &m->gen, (size_t)m->ctx * 4))
         return -1;
+    m->part_cap = head_grid;
     // RoPE tables with the reference's own formulas (host libm, so the values are the reference's)
     const int half = m->hs / 2;
     std::vector<float> c((size_t)m->ctx * half), s((size_t)m->ctx * half);
@@ -835,6 +869,8 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     prefill_att_slices(p0 + M, &pa.att_sl, &pa.att_smax);
     pa.att_ml = m->pf_ml;
     pa.att_acc = m->pf_acc;
+    pa.strict = m->strict;
+    pa.xb = m->pf_y; // strict attention rows: the QKV GEMM output is consumed by then
     HIP_OR_FAIL("llm_prefill", launch_p_embed(pa, m->st));
     PgemmArgs g;
     memset(&g, 0, sizeof g);
@@ -1287,6 +1323,24 @@ extern "C" int llm_sampler_state(llm_model *m, unsigned long long *rng) {
     *rng = st.rng;
     return 0;
 }
+
+extern "C" int llm_set_strict(llm_model *m, int on) {
+    if (!m) return -1;
+    hipSetDevice(m->device);
+    HIP_OR_FAIL("llm_set_strict", hipStreamSynchronize(m->st));
+    if ((on != 0) == (m->strict != 0)) return 0;
+    m->strict = on != 0;
+    if (pick_shapes(m)) return -1;
+    // the captured step graphs hold the other mode's kernels and shapes
+    for (hipGraphExec_t *g : {&m->g_plain, &m->g_hist, &m->g_plain_s, &m->g_hist_s})
+        if (*g) {
+            hipGraphExecDestroy(*g);
+            *g = nullptr;
+        }
+    return 0;
+}
+
+extern "C" int llm_get_strict(const llm_model *m) { return m ? m->strict : -1; }
 
 extern "C" int llm_set_prefill(llm_model *m, int on) {
     if (!m) return -1;

@@ -35,6 +35,8 @@ struct ProwArgs {           // per-token elementwise kernels
     int8_t *oq;             // [M][width] quantized output (the next GEMM's input)
     float *os;              // [M][width / gs]
     int n_heads, n_kv;
+    int strict;             // 1: reference order (sequential RMSNorm sum, reference-order attention, libm expf)
+    float *xb;              // strict attention: [M][dim] output rows before quantization
     // attention slices: positions of token m in slices of att_sl, at most att_smax per token; partials
     // ml [M][n_heads][att_smax][2] (max, sum of exp) and acc [M][n_heads][att_smax][hs]
     int att_sl, att_smax;

@@ -227,7 +227,15 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
         sv[i] = v;
         part += v * v;
     }
-    float ss = block_sum(part, sv + n);
+    float ss;
+    if (a.strict) { // one running sum in element order (qwen.c:339, runq.c:396-398)
+        __syncthreads();
+        if (threadIdx.x == 0) sv[n] = seq_sum_squares(sv, n);
+        __syncthreads();
+        ss = sv[n];
+    } else {
+        ss = block_sum(part, sv + n);
+    }
     ss /= (float)n;
     ss += a.eps;
     ss = 1.0f / sqrtf(ss);
@@ -307,7 +315,7 @@ __global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
                 float h[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const float sig = 1.0f / (1.0f + expf(-g[e]));
+                    const float sig = 1.0f / (1.0f + (a.strict ? ref_expf(-g[e]) : expf(-g[e])));
                     const float gs = g[e] * sig;
                     h[e] = gs * u[e];
                 }
@@ -576,6 +584,24 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
     block_quantize(row, a.dim, a.gs, a.qflavor, a.oq + (size_t)m * a.dim, a.os + (size_t)m * (a.dim / a.gs));
 }
 
+// Reference-order causal attention: block (h, m) is query head h of token m over positions 0 .. p0 + m
+// (attn_strict_head); the fp32 output row goes to xb[m], quantized afterwards by k_p_quant_rows.
+__global__ void __launch_bounds__(256) k_p_attn_strict(ProwArgs a) {
+    extern __shared__ __align__(16) float sm[];
+    const int h = blockIdx.x, m = blockIdx.y, hs = a.head_size, kv_mul = a.n_heads / a.n_kv;
+    attn_strict_head(a.q + (size_t)m * a.dim + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs,
+                     a.p0 + m + 1, sm, a.xb + (size_t)m * a.dim + (size_t)h * hs);
+}
+
+// int8 quantization of the rows xb[m] (qwen.c:549, runq.c:571) into the o projection's input
+__global__ void __launch_bounds__(256) k_p_quant_rows(ProwArgs a) {
+    extern __shared__ __align__(16) float sv[];
+    const int m = blockIdx.x, n = a.dim;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.xb[(size_t)m * n + i];
+    __syncthreads();
+    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
+}
+
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(k_p_embed, dim3(a.M), dim3(256), 0, st, a);
     return hipGetLastError();
@@ -603,6 +629,17 @@ hipError_t launch_p_swiglu_quant(const ProwArgs &a, hipStream_t st) {
 }
 hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv, hs = a.head_size;
+    if (a.strict) {
+        const size_t lds = attn_strict_lds_floats(hs, a.p0 + a.M, 256) * 4;
+        if (hs % 4 || ((uintptr_t)a.kc & 15) || a.kv_dim % 4 || a.dim % 4 || a.dim % a.gs || !a.xb ||
+            ((uintptr_t)a.oq & 3) || lds > 65536 || a.n_heads % a.n_kv)
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_p_attn_strict, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(k_p_quant_rows, dim3(a.M), dim3(256), (size_t)a.dim * 4, st, a);
+        return hipGetLastError();
+    }
     if (kv_mul * hs > 1024 || hs % 4 || hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) ||
         ((uintptr_t)a.vc & 15) || ((uintptr_t)a.oq & 3) || ((uintptr_t)a.att_acc & 15) || a.kv_dim % 4 ||
         a.dim % 4 || a.dim % a.gs || a.att_sl < ATT_SUB || a.att_sl % 16 || a.att_smax < 1 ||

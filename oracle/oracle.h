@@ -33,6 +33,7 @@ void or_matvec_runq_groups(int32_t *ival, const int8_t *wq, const int8_t *xq, in
 void or_rmsnorm(float *o, const float *x, const float *w, int n, float eps); /* qwen.c:337-344, runq.c:394-407 */
 void or_set_norm_ways(int k); /* 1 = reference order (default); k partial sums of x^2 (tolerance test only) */
 void or_softmax(float *x, int n);                                      /* qwen.c:346-352, runq.c:409-427 */
+void or_expf(const float *x, int n, float *y); /* the C library's expf, as qwen.c:350 / 560 and runq.c:420 / 592 call it */
 void or_rope_angles(float *c, float *s, int hs, int pos, float theta); /* qwen.c:503-508 */
 void or_rope_neox(float *v, int n_heads, int hs, const float *c, const float *s); /* qwen.c:478-488 */
 void or_rope_runq(float *q, float *k, int dim, int kv_dim, int hs, int pos); /* runq.c:506-521 */

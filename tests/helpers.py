@@ -51,6 +51,7 @@ def oracle():
         L.or_matvec_runq_groups.argtypes = [vp, vp, vp, i32, i32, i32]
         L.or_rmsnorm.argtypes = [vp, vp, vp, i32, C.c_float]
         L.or_softmax.argtypes = [vp, i32]
+        L.or_expf.argtypes = [vp, i32, vp]
         L.or_rope_angles.argtypes = [vp, vp, i32, i32, C.c_float]
         L.or_rope_neox.argtypes = [vp, i32, i32, vp, vp]
         L.or_rope_runq.argtypes = [vp, vp, i32, i32, i32, i32]
@@ -123,7 +124,7 @@ def q4_weights(rng, d, n):
 
 
 def f16_scales(rng, count, special_rows=0, ng=1):
-    """random sign, exponent 5..10, random mantissa (hls4/matvec4_tb.cpp:309-318); with special_rows,
+    """random sign, exponent 5..10, random mantissa (hls4/matvec4_tb.cpp:88-97); with special_rows,
     row i's scales get exponent field i % 31: zero, subnormals, up to 65504"""
     if special_rows:
         e = (np.arange(count) // ng) % 31
@@ -142,7 +143,7 @@ def unpack_q4(w, d, n):
 
 
 def exact_terms(wvals, ws_f32, xq, xs, gs=32):
-    """per-row exact reference in float64 and the sum of |term| (hls4/matvec4_tb.cpp:286-296)"""
+    """per-row exact reference in float64 and the sum of |term| (hls4/matvec4_tb.cpp:67-77)"""
     d, n = wvals.shape
     ng = n // gs
     isum = (wvals.reshape(d, ng, gs).astype(np.int64) * xq.reshape(1, ng, gs).astype(np.int64)).sum(2)

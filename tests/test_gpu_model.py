@@ -1,15 +1,17 @@
-"""The device-resident token loop against the oracle (MI355X).
+"""The device-resident token loop in its fast mode against the oracle (MI355X).
 
-Bar (written here): logits within 1e-3 relative to the largest |logit| of the
-position, greedy ids identical; a divergence is only accepted at a near-tied argmax, reported with its gap.
-Golden fixtures: the reference binaries' own logits and ids (tests/golden/tiny_*).
-
-Deep models: the activations are re-quantized to int8 four times per layer, and a value that lands within
-fp32 rounding of a rounding boundary flips one int8 step when the fp32 sums are taken in another order
-(the device's tree vs the reference's sequential loop).  One flip moves the logits by ~1e-3 of their
-scale at once, so for models with several layers the bar is: every position at or under 1e-3 until the
-first such event, the median position under 1e-4, no position over 2e-2, and identical greedy ids (or a
-divergence at a near tie, whose gap is reported)."""
+The parity mode is the strict mode (tests/test_gpu_strict.py): bitwise equal to the reference at every
+configuration's full workload.  The fast mode (the default for .qwb models) sums groups, RMSNorm's squares
+and softmax terms in trees, so it is a different fp32 summation order, and these tests hold it to:
+  - tiny models (2 layers): logits within 1e-3 of the reference binaries' own (tests/golden/tiny_*), ids equal;
+  - deeper models (deep_bar): the activations are re-quantized to int8 four times per layer, and a value that
+    lands within fp32 rounding of a rounding boundary flips one int8 step when its sum is taken in another
+    order.  One flip moves the logits by ~1e-3 of their scale at once and later layers spread it, so the bar
+    is: every position within 1e-5 until the first such event (a position over 1e-4), no position over 2e-2,
+    and identical greedy ids, or a divergence where the oracle's own top-2 gap is at most twice the logit
+    error measured at that position (the reordering could have swapped them).
+With the reference's own arithmetic, reordering only the group sum spreads a 24-layer Qwen2-0.5B-shape model's
+logits by ~2e-2 (tests/test_oracle.py): that is the fast mode's expected deviation at full depth."""
 import json
 import os
 import subprocess
@@ -88,13 +90,15 @@ def compare_with_oracle(path, prompt, max_new, ctx, runq=False):
     return ids_o, ids_g, errs, div, gap
 
 
-def deep_bar(errs, div, gap, ids_o, ids_g):
-    """exact (< 1e-5) until the first int8 boundary event, bounded after it, ids identical or a near tie"""
+def deep_bar(errs, div, gap, ids_o, ids_g, n_prompt):
+    """exact (< 1e-5) until the first int8 boundary event, bounded after it, ids identical or a divergence
+    that the measured error explains"""
     first = next((i for i, e in enumerate(errs) if e > 1e-4), len(errs))
     assert all(e < 1e-5 for e in errs[:first]), errs
     assert max(errs) < 2e-2, errs
-    if div is not None:  # accepted only where the oracle's top two logits are closer than the measured error
-        assert gap is not None and gap < 2e-2, (div, gap, ids_o, ids_g)
+    if div is not None:  # the oracle's top two logits closer than the error measured at that position
+        at = n_prompt - 1 + div
+        assert gap is not None and gap <= 2 * errs[at], (div, gap, errs[at], ids_o, ids_g)
 
 
 def test_qwen_shapes_c3_two_layers(tmp_path):
@@ -104,7 +108,7 @@ def test_qwen_shapes_c3_two_layers(tmp_path):
     hid = walk_qwb(p)["head_ids"]
     prompt = [int(v) for v in np.random.default_rng(5).choice(hid, 24, replace=False)]
     ids_o, ids_g, errs, div, gap = compare_with_oracle(p, prompt, 16, 64)
-    deep_bar(errs, div, gap, ids_o, ids_g)
+    deep_bar(errs, div, gap, ids_o, ids_g, len(prompt))
 
 
 def test_qwen_shapes_c5_one_layer(tmp_path):
@@ -112,7 +116,7 @@ def test_qwen_shapes_c5_one_layer(tmp_path):
     p = synth("qwb", str(tmp_path / "c5l1.qwb"), "c5", 22, "layers=1", "vocab=8192", "head_k=8192")
     prompt = [int(v) for v in np.random.default_rng(6).integers(0, 8192, 8)]
     ids_o, ids_g, errs, div, gap = compare_with_oracle(p, prompt, 6, 32)
-    deep_bar(errs, div, gap, ids_o, ids_g)
+    deep_bar(errs, div, gap, ids_o, ids_g, len(prompt))
 
 
 def test_runq_c1_shape(tmp_path):
@@ -120,7 +124,7 @@ def test_runq_c1_shape(tmp_path):
     p = synth("bin", str(tmp_path / "c1.bin"), "c1", 23)
     prompt = [1] + [int(v) for v in np.random.default_rng(7).integers(3, 32000, 7)]
     ids_o, ids_g, errs, div, gap = compare_with_oracle(p, prompt, 33, 0, runq=True)
-    deep_bar(errs, div, gap, ids_o, ids_g)
+    deep_bar(errs, div, gap, ids_o, ids_g, len(prompt))
 
 
 @pytest.mark.parametrize("shape", [("dim=128", "heads=4", "kv_heads=2"), ("dim=256", "heads=4", "kv_heads=1"),

@@ -2,7 +2,7 @@
 
 Bars: int8 quantization and int32 group sums bit-exact; fpga_matvec (runq flavour) bit-exact, the reference
 testbench's bar (hls/matvec_tb.cpp:82-83); fpga_matvec4 (qwen flavour) within |out - exact| <= 1e-5 *
-sum_g |term_g|, the reference testbench's bar (hls4/matvec4_tb.cpp:19, 297-298)."""
+sum_g |term_g|, the reference testbench's bar (hls4/matvec4_tb.cpp:19, 67-79)."""
 import ctypes as C
 import os
 
@@ -105,7 +105,7 @@ def test_matvec4_testbench_bar(drv, n, d, bits):
 
 @pytest.mark.parametrize("bits", [4, 8])
 def test_matvec4_special_fp16_scales(drv, bits):
-    """row i's scales have exponent field i % 31: zero, subnormals, up to 65504 (hls4/matvec4_tb.cpp:307-318)"""
+    """row i's scales have exponent field i % 31: zero, subnormals, up to 65504 (hls4/matvec4_tb.cpp:88-97, 143-144)"""
     rng = np.random.default_rng(77 + bits)
     n, d = 64, 31
     w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
@@ -224,7 +224,7 @@ def test_argument_errors(drv, capfd):
 
 def test_forced_timeout_reports_minus_one(capfd):
     """FPGA_TIMEOUT_MS=0: the completion wait gives up at once and the call fails like the reference's 5 s
-    ap_done time-out (matvec_fpga.cpp:229-233); the kernel itself runs normally"""
+    ap_done time-out (matvec_fpga.cpp:156-170, 226-230); the kernel itself runs normally"""
     P = pkg()
     L = P.lib()
     L.fpga_close()
