@@ -149,6 +149,13 @@ int mvh_sample(const float *logits, int n, int count, float temperature, float t
  * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d] */
 int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
                      int bits, int gs, int rb, float *y);
+/* mvh_sample with no device allocation: no counterpart in the reference; for callers that cannot allocate
+ * device memory (tight serving loops, harnesses that forbid hipMalloc).  Same arguments, draws and RNG state as
+ * mvh_sample, but every device buffer lives in a fixed array inside the library (about 9 MiB per GPU, held
+ * until the process ends): n <= 262144, count <= 4096 and count * (n rounded up to 4) <= 2^21, otherwise -1
+ * with a message.  Calls that overlap on one GPU (several host threads) share that array and race. */
+int mvh_sample_noalloc(const float *logits, int n, int count, float temperature, float topp,
+                       unsigned long long *rng, int *rows);
 /* expf as the reference's C library evaluates it (the strict mode's softmax and SiLU), over n floats: on the
  * device (n <= 2^26), and the same restatement compiled for the host CPU (no GPU involved) */
 int mvh_ref_expf(const float *x, int n, float *y);

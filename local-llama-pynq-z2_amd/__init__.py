@@ -84,6 +84,7 @@ def lib():
     L.llm_set_sampler.argtypes = [vp, C.c_float, C.c_float, C.c_ulonglong]
     L.llm_sampler_state.argtypes = [vp, C.POINTER(C.c_ulonglong)]
     L.mvh_sample.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
+    L.mvh_sample_noalloc.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
     L.mvh_ref_expf.argtypes = [vp, i32, vp]
     L.mvh_ref_expf_host.argtypes = [vp, i32, vp]
     L.llm_set_strict.argtypes = [vp, i32]
@@ -131,14 +132,15 @@ def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16):
     return y
 
 
-def sample(logits, temperature, topp, seed):
+def sample(logits, temperature, topp, seed, noalloc=False):
     """The on-device sampler on caller logits [count, n] (or [n]), drawn in order with one RNG state seeded by
-    `seed`: (rows, the advanced RNG state)."""
+    `seed`: (rows, the advanced RNG state).  noalloc: the entry point that allocates no device memory."""
     lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
     rows = np.empty(lg.shape[0], np.int32)
     st = C.c_ulonglong(seed)
-    if lib().mvh_sample(_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)) != 0:
-        raise RuntimeError("mvh_sample failed")
+    fn = lib().mvh_sample_noalloc if noalloc else lib().mvh_sample
+    if fn(_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)) != 0:
+        raise RuntimeError("mvh_sample_noalloc failed" if noalloc else "mvh_sample failed")
     return rows, st.value
 
 
