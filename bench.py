@@ -6,17 +6,20 @@ with seeded head_ids; seeded N(0, 0.02) random-init weights written by host/synt
 greedy, batch 1.  A step is one decode position: the whole forward() plus the argmax on the device, one
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
-  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu]
-  roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes:
-    rocprofv3 --pmc FETCH_SIZE -d D/fetch -- python bench.py --counters --profile-steps 4
-    rocprofv3 --pmc WRITE_SIZE -d D/write -- python bench.py --counters --profile-steps 4
-    python bench.py --traffic-from D ...
+  python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu] [--no-counters]
+  The default run (c3) also measures the Qwen2-7B shape (c5) and reports it as the sub-record "c5".
+  roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes that the
+  run starts itself as child processes (FETCH_SIZE, then WRITE_SIZE, over `bench.py --counters`: a calibration
+  copy of 1 GiB, then the prompt and 4 decode steps as eager launches), or from earlier passes:
+    python bench.py --traffic-from D ...      (D/fetch, D/write: rocprofv3 -d directories of the two passes)
   (c4: the 512-token prompt as one batched int8-MFMA prefill, timed over --steps repetitions)
 
 Also reported: per-kernel roofline (each kernel kind's device time inside the replayed step graph, from HIP
-events around graph replays with and without that kind's launches, and its algorithmic bytes per launch),
-the greedy ids against the reference's own qwen.c, and that qwen.c (built with OpenMP, -O3 -ffast-math,
-oracle/_ref/qwen_fast) timed on this host's cores on a bounded sample of the workload."""
+events around graph replays with and without that kind's launches, and its algorithmic bytes per launch);
+the greedy workload in the fast mode and in the strict (reference-order) mode against the reference's own
+qwen.c / runq.c built strict IEEE (ids, and every position's logits: bitwise for the strict mode); and the
+reference's OpenMP build (oracle/_ref/qwen_fast, -O3 -ffast-math) timed on this host over the same workload,
+with this host's logical CPU count and model name."""
 import argparse
 import importlib.util
 import json
@@ -97,54 +100,92 @@ def ref_args(cfg, path, prompt, n_new):
     return [path, "--ids", ids, "-t", "0", "-n", str(len(prompt) - 1 + n_new)]
 
 
+def host_cpu():
+    """(logical CPUs of this host, lscpu model name)"""
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        m = re.search(r"Model name:\s*(.+)", out)
+        model = m.group(1).strip() if m else None
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return os.cpu_count(), model
+
+
+def omp_threads():
+    """OpenMP threads for the reference's CPU runs: this host's OMP_NUM_THREADS when set (the CPU share a GPU
+    job gets on a shared host), else every logical CPU"""
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
 def cpu_baseline(cfg, path, prompt, n_new):
-    """the reference's qwen.c / runq.c (OpenMP build) on this host: bounded sample of the same workload"""
+    """the reference's qwen.c / runq.c (OpenMP build) on this host over the workload: the prompt and n_new greedy
+    tokens, decode rate in qwen.c's definition"""
     exe = os.path.join(REPO, "oracle", "_ref", "qwen_fast" if cfg["ref"] == "qwen" else "runq_ids_fast")
     if not os.path.exists(exe):
         return None
-    threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
+    threads = omp_threads()
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
     t = time.time()
-    r = subprocess.run([exe] + ref_args(cfg, path, prompt, n_new), capture_output=True, text=True, env=env, timeout=600)
+    r = subprocess.run([exe] + ref_args(cfg, path, prompt, n_new), capture_output=True, text=True, env=env, timeout=900)
     wall = time.time() - t
     m = re.search(r"generated: (\d+) tokens, ([0-9.]+) tok/s", r.stderr)
     if r.returncode != 0 or not m:
         log(f"cpu baseline failed: {r.stderr[-400:]}")
         return None
     src = "qwen.c" if cfg["ref"] == "qwen" else "runq.c"
+    nproc, model = host_cpu()
     return {"value": float(m.group(2)), "unit": "tok/s", "cores": threads, "kind": "reference",
-            "sample": f"{src} (OpenMP, -O3 -ffast-math -march=x86-64-v3) on the same .{cfg['fmt']}: {len(prompt)}-token "
-                      f"prompt + {int(m.group(1))} greedy tokens, decode rate in qwen.c's definition ({wall:.1f} s wall)"}
+            "nproc": nproc, "cpu_model": model,
+            "sample": f"{src} (OpenMP, {threads} threads = this host's OMP_NUM_THREADS, -O3 -ffast-math "
+                      f"-march=x86-64-v3) on the same .{cfg['fmt']}: {len(prompt)}-token prompt + {int(m.group(1))} "
+                      f"greedy tokens, decode rate in qwen.c's definition ({wall:.1f} s wall)"}
 
 
-def greedy_parity(cfg, path, prompt, n_new, ids_gpu, logits_gpu):
-    """the reference's qwen.c / runq.c built strict IEEE (oracle/_ref/qwen, runq_ids): its greedy ids and
-    --logits dump against the device run; a divergence is reported with the reference's top-2 logit gap"""
+def reference_run(cfg, path, prompt, n_new, n_logits):
+    """the reference's qwen.c / runq.c built strict IEEE (oracle/_ref/qwen, runq_ids) over the workload: its
+    greedy ids and its --logits dump of every position"""
     exe = os.path.join(REPO, "oracle", "_ref", "qwen" if cfg["ref"] == "qwen" else "runq_ids")
     if not os.path.exists(exe):
         return None
     dump = os.path.join(os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench"), "ref.logits")
-    threads = int(os.environ.get("OMP_NUM_THREADS") or min(16, os.cpu_count() or 1))
     r = subprocess.run([exe] + ref_args(cfg, path, prompt, n_new) + ["--logits", dump], capture_output=True, text=True,
-                       timeout=900, env=dict(os.environ, OMP_NUM_THREADS=str(threads)))
+                       timeout=900, env=dict(os.environ, OMP_NUM_THREADS=str(omp_threads())))
     if r.returncode != 0:
+        log(f"reference run failed: {r.stderr[-400:]}")
         return None
-    ids_ref = [int(v) for v in r.stdout.strip().split(",") if v]
-    ref = np.fromfile(dump, np.float32).reshape(-1, logits_gpu.shape[1])
+    ids = [int(v) for v in r.stdout.strip().split(",") if v]
+    return ids, np.fromfile(dump, np.float32).reshape(-1, n_logits)
+
+
+def fast_parity(ref, prompt, ids_gpu, logits_gpu):
+    """the fast mode's greedy ids and logits against the reference run; a divergence is reported with the
+    reference's top-2 logit gap"""
+    ids_ref, lg_ref = ref
     n = min(len(ids_ref), len(ids_gpu))
     div = next((i for i in range(n) if ids_ref[i] != ids_gpu[i]), None)
-    rows = min(len(ref), len(logits_gpu))
+    rows = min(len(lg_ref), len(logits_gpu))
     upto = rows if div is None else len(prompt) + div  # positions on the shared token path
-    errs = [float(np.abs(logits_gpu[p] - ref[p]).max() / np.abs(ref[p]).max()) for p in range(upto)]
-    out = {"reference": ("qwen.c" if cfg["ref"] == "qwen" else "runq.c") + " strict IEEE build", "tokens_compared": n,
-           "identical": div is None,
-           "first_divergence": div, "logit_rel_err_max": max(errs) if errs else None,
+    errs = [float(np.abs(logits_gpu[p] - lg_ref[p]).max() / np.abs(lg_ref[p]).max()) for p in range(upto)]
+    out = {"mode": "fast (tree sums)", "reference": "strict IEEE build", "tokens_compared": n,
+           "identical": div is None, "first_divergence": div,
+           "logit_rel_err_max": max(errs) if errs else None,
            "logit_rel_err_median": float(np.median(errs)) if errs else None}
     if div is not None:
-        row = ref[len(prompt) - 1 + div]
+        row = lg_ref[len(prompt) - 1 + div]
         top = np.sort(row)[-2:]
         out["reference_top2_gap_rel"] = float((top[1] - top[0]) / np.abs(row).max())
     return out
+
+
+def strict_parity(ref, ids_gpu, logits_gpu, tok_s):
+    """the strict mode's greedy ids and logits against the reference run: bit for bit"""
+    ids_ref, lg_ref = ref
+    rows = min(len(lg_ref), len(logits_gpu))
+    same = rows == len(lg_ref) == len(logits_gpu) and all(np.array_equal(logits_gpu[p], lg_ref[p]) for p in range(rows))
+    return {"mode": "strict (reference order)", "reference": "strict IEEE build", "positions": int(len(lg_ref)),
+            "tokens": len(ids_ref), "bitwise_identical_logits": bool(same), "identical_ids": list(ids_ref) == list(ids_gpu),
+            "tok_s": round(tok_s, 1)}
 
 
 # HIP kernel of each step kernel kind (.qwb models: int4 layers, int8 head), as the start of the name rocprofv3
@@ -239,6 +280,151 @@ def prefill_bench(a, cfg, path, prompt):
     print(json.dumps(out), flush=True)
 
 
+def prompt_for(cfg, path):
+    if cfg["fmt"] == "qwb":
+        hid = head_ids_of(path)
+        return [int(v) for v in np.random.default_rng(cfg["seed"]).choice(hid, cfg["prompt"], replace=False)]
+    # runq: seeded ids from [2, vocab) (1 is BOS, which stops the generation)
+    with open(path, "rb") as f:
+        vocab = int(abs(np.frombuffer(f.read(64), np.int32, 1, 8 + 5 * 4)[0]))
+    return [int(v) for v in np.random.default_rng(cfg["seed"]).integers(2, vocab, cfg["prompt"])]
+
+
+def counter_traffic(config, kind):
+    """roofline.traffic: HBM bytes per launch of `kind` from two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE) over `bench.py --counters` as child processes, each pass with its own time limit; None when
+    rocprofv3 is absent or a pass fails.  The passes launch the step's kernels eagerly (a pass over replayed
+    step graphs once ended in a segmentation fault inside the profiled process)."""
+    import shutil
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None
+    d = os.path.join(os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench"), f"pmc_{config}")
+    shutil.rmtree(d, ignore_errors=True)
+    env = dict(os.environ, TMPDIR="/tmp")
+    for sub, counter in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        cmd = ["timeout", "-s", "KILL", "180", prof, "--pmc", counter, "--output-format", "csv", "-d",
+               os.path.join(d, sub), "-o", sub, "--", sys.executable, "-u", os.path.abspath(__file__), "--counters",
+               "--config", config, "--profile-steps", "4"]
+        log(f"counter pass {counter}")
+        r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+        if r.returncode != 0:
+            log(f"counter pass {counter} failed (status {r.returncode}): {r.stderr[-300:]}")
+            return None
+    return traffic_from(d, kind)
+
+
+def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters):
+    """one configuration: timed greedy decode steps (fast mode), per-kernel in-graph roofline, the fast and
+    the strict mode against the reference's strict build over cpu_tokens greedy tokens, and the reference's
+    OpenMP build timed on this host"""
+    cfg = CONFIGS[name]
+    path = model_file(cfg)
+    prompt = prompt_for(cfg, path)
+    P = load_pkg()
+    t = time.time()
+    m = P.Model(path, cfg["ctx"])
+    log(f"[{name}] model resident in {time.time() - t:.1f} s: {m.info.weight_bytes / 2**20:.0f} MiB of tiled weights, "
+        f"{m.info.gemv_bytes_per_token / 1e6:.2f} MB GEMV bytes per token")
+    if len(prompt) + 1 + max(steps, warmup, profile_steps, cpu_tokens) >= m.info.ctx:
+        raise SystemExit("steps do not fit the context")
+    import torch
+
+    # greedy run of the parity workload (fast mode), with every position's logits
+    gen = m.generate(prompt, cpu_tokens, logits=True)
+    ids_fast, lg_fast = [int(v) for v in gen["ids"]], gen["logits"]
+    log(f"[{name}] greedy run: {len(ids_fast)} tokens, device decode {gen['timing'].decode_ms:.1f} ms")
+
+    decoding = "argmax"
+    if a.sample:
+        t_, p_, s_ = a.sample.split(",")
+        m.set_sampler(float(t_), float(p_), int(s_))
+        decoding = f"sampler temperature {float(t_)} top-p {float(p_)} seed {int(s_)}"
+
+    # warmup: W steps after the prompt, then back to the prompt's end for the timed steps
+    m.generate(prompt, 1)
+    if warmup:
+        m.decode_replay(warmup)
+    m.generate(prompt, 1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev_ms = m.decode_replay(steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    tok_s = steps / wall
+    log(f"[{name}] timed {steps} decode steps: {wall * 1e3:.2f} ms wall, {ev_ms:.2f} ms by events -> {tok_s:.1f} tok/s")
+
+    # per-kernel roofline: each kernel kind's time inside the replayed step graph
+    m.set_sampler(0.0)
+    m.generate(prompt, 1)
+    eager = {s["name"]: s for s in m.profile(profile_steps)}
+    m.generate(prompt, 1)
+    stats, step_ms = m.profile_graph(profile_steps, rounds=3)
+    total = sum(s["total_ms"] for s in stats)
+    log(f"[{name}] in-graph kernel times over {profile_steps} replayed steps (median step {step_ms * 1e3:.1f} us, "
+        f"sum of kinds {total / profile_steps * 1e3:.1f} us):")
+    for s in sorted(stats, key=lambda s: -s["total_ms"]):
+        avg = s["total_ms"] / s["launches"]
+        e = eager.get(s["name"])
+        e_us = f"{e['total_ms'] / e['launches'] * 1e3:8.2f}" if e else "     -  "
+        log(f"  {s['name']:12s} {s['launches']:6d} launches  avg {avg * 1e3:8.2f} us (eager {e_us} us)"
+            f"  {s['total_ms'] / total * 100:5.1f}%  {s['bytes_per_launch'] / 1e6:8.3f} MB"
+            f"  {s['bytes_per_launch'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
+    dom = max(stats, key=lambda s: s["total_ms"])
+    dom_avg_s = dom["total_ms"] / dom["launches"] * 1e-3
+    achieved = dom["bytes_per_launch"] / dom_avg_s / 1e9
+    gemv = [s for s in stats if s["name"].endswith("_gemv")]
+    gemv_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in gemv)
+    gemv_s = sum(s["total_ms"] for s in gemv) * 1e-3
+    per_kernel = {s["name"]: {"avg_us": round(s["total_ms"] / s["launches"] * 1e3, 3),
+                              "GB_s": round(s["bytes_per_launch"] / (s["total_ms"] / s["launches"] * 1e-3) / 1e9, 1)}
+                  for s in stats}
+
+    # the strict (reference-order) mode: the same greedy workload, and its decode rate
+    m.set_strict(True)
+    gs = m.generate(prompt, cpu_tokens, logits=True)
+    ids_strict, lg_strict = [int(v) for v in gs["ids"]], gs["logits"]
+    m.generate(prompt, 1)
+    sst = min(steps, 32)
+    strict_tok_s = sst / (m.decode_replay(sst) * 1e-3)
+    log(f"[{name}] strict mode: {strict_tok_s:.1f} tok/s")
+    n_logits = m.info.n_logits
+    m.close()
+
+    ref = None if a.no_cpu else reference_run(cfg, path, prompt, cpu_tokens, n_logits)
+    traffic = None
+    if a.traffic_from:
+        traffic = traffic_from(a.traffic_from, dom["name"])
+    elif counters:
+        traffic = counter_traffic(name, dom["name"])
+    if traffic:
+        log(f"[{name}] traffic of {dom['name']}: {traffic['fetch'] / 1e6:.3f} MB fetched + "
+            f"{traffic['write'] / 1e6:.3f} MB written per launch (counter factors {traffic['fetch_factor']:.3f} / "
+            f"{traffic['write_factor']:.3f})")
+    cpu = None if a.no_cpu else cpu_baseline(cfg, path, prompt, cpu_tokens)
+    return {
+        "metric": cfg["metric"],
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(wall / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic: seeded N(0,0.02) random-init weights (" + ("Q4_0 layers, Q8_0 head" if cfg["fmt"] == "qwb"
+                 else "Q8_0 with fp32 scales") + "), seeded prompt ids",
+        "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
+                   "decoding": decoding, "ctx": m.info.ctx, "batch": 1},
+        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
+                     "traffic": round(traffic["fetch"] + traffic["write"]) if traffic else None,
+                     "avg_launch_us": round(dom_avg_s * 1e6, 3), "bytes_per_launch": round(dom["bytes_per_launch"])},
+        "gemv_all": {"achieved": round(gemv_bytes / gemv_s / 1e9, 1), "unit": "GB/s",
+                     "frac": round(gemv_bytes / gemv_s / 1e9 / PEAK_HBM, 4),
+                     "share_of_step": round(sum(s["total_ms"] for s in gemv) / total, 4)},
+        "kernels_in_graph": per_kernel,
+        "cpu_baseline": cpu,
+        "greedy_vs_reference": fast_parity(ref, prompt, ids_fast, lg_fast) if ref else None,
+        "strict_vs_reference": strict_parity(ref, ids_strict, lg_strict, strict_tok_s) if ref else None,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,8 +432,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--profile-steps", type=int, default=32)
-    ap.add_argument("--cpu-tokens", type=int, default=32)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=None,
+                    help="greedy tokens of the parity and CPU-baseline runs (default: the workload's)")
+    ap.add_argument("--no-cpu", action="store_true", help="no reference runs (parity lines, CPU baseline)")
+    ap.add_argument("--no-counters", action="store_true", help="no rocprofv3 counter passes (roofline.traffic null)")
+    ap.add_argument("--no-c5", action="store_true", help="no Qwen2-7B-shape sub-record in the default run")
     ap.add_argument("--sample", default=None, metavar="T,P,SEED",
                     help="decode with the on-device sampler (temperature, top-p, seed) instead of the argmax")
     ap.add_argument("--calib", action="store_true", help="run the counter calibration copy first")
@@ -262,14 +451,6 @@ def main():
         sys.exit(2)
     cfg = CONFIGS[a.config]
     steps = a.steps or cfg["new"]
-    path = model_file(cfg)
-    if cfg["fmt"] == "qwb":
-        hid = head_ids_of(path)
-        prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).choice(hid, cfg["prompt"], replace=False)]
-    else:  # runq: seeded ids from [2, vocab) (1 is BOS, which stops the generation)
-        with open(path, "rb") as f:
-            vocab = int(abs(np.frombuffer(f.read(64), np.int32, 1, 8 + 5 * 4)[0]))
-        prompt = [int(v) for v in np.random.default_rng(cfg["seed"]).integers(2, vocab, cfg["prompt"])]
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
@@ -277,6 +458,8 @@ def main():
     if a.calib or a.counters:
         calib_copy()
     if a.counters:
+        path = model_file(cfg)
+        prompt = prompt_for(cfg, path)
         P = load_pkg()
         m = P.Model(path, cfg["ctx"])
         for pos, t in enumerate(prompt):
@@ -286,96 +469,15 @@ def main():
         log(f"counter pass: {len(prompt)} eager positions + {a.profile_steps} profiled steps")
         return
     if a.config == "c4":
-        return prefill_bench(a, cfg, path, prompt)
-    P = load_pkg()
-    t = time.time()
-    m = P.Model(path, cfg["ctx"])
-    log(f"model resident in {time.time() - t:.1f} s: {m.info.weight_bytes / 2**20:.0f} MiB of tiled weights, "
-        f"{m.info.gemv_bytes_per_token / 1e6:.2f} MB GEMV bytes per token")
-    ctx_used = m.info.ctx
-    if len(prompt) + 1 + max(steps, a.warmup, a.profile_steps) >= m.info.ctx:
-        raise SystemExit("steps do not fit the context")
-
-    # greedy run of the workload (also the parity line against the reference below)
-    gen = m.generate(prompt, steps, logits=True)
-    ids_gpu = [int(v) for v in gen["ids"]]
-    log(f"greedy run: {len(ids_gpu)} tokens, device decode {gen['timing'].decode_ms:.1f} ms "
-        f"({(gen['timing'].n_forward - len(prompt)) / gen['timing'].decode_ms * 1e3:.0f} tok/s with host stop checks)")
-
-    # --sample: the timed steps draw with the on-device sampler (the greedy run above stays the parity line)
-    decoding = "argmax"
-    if a.sample:
-        t_, p_, s_ = a.sample.split(",")
-        m.set_sampler(float(t_), float(p_), int(s_))
-        decoding = f"sampler temperature {float(t_)} top-p {float(p_)} seed {int(s_)}"
-        log(f"decoding with the on-device {decoding}")
-
-    # warmup: W steps after the prompt, then back to the prompt's end for the timed steps
-    m.generate(prompt, 1)
-    if a.warmup:
-        m.decode_replay(a.warmup)
-    m.generate(prompt, 1)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev_ms = m.decode_replay(steps)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    tok_s = steps / wall
-    log(f"timed {steps} decode steps: {wall * 1e3:.2f} ms wall, {ev_ms:.2f} ms by events -> {tok_s:.1f} tok/s")
-
-    # per-kernel roofline: each kernel kind's time inside the replayed step graph (HIP events around graph
-    # replays with and without that kind's launches, on the library's stream); eager per-launch event times,
-    # which add launch and event overhead to every kernel, are logged beside them
-    m.set_sampler(0.0)  # the per-kernel figures are those of the argmax step
-    m.generate(prompt, 1)
-    eager = {s["name"]: s for s in m.profile(a.profile_steps)}
-    m.generate(prompt, 1)
-    stats, step_ms = m.profile_graph(a.profile_steps, rounds=3)
-    total = sum(s["total_ms"] for s in stats)
-    log(f"in-graph kernel times over {a.profile_steps} replayed steps (median step {step_ms * 1e3:.1f} us, "
-        f"sum of kinds {total / a.profile_steps * 1e3:.1f} us):")
-    for s in sorted(stats, key=lambda s: -s["total_ms"]):
-        avg = s["total_ms"] / s["launches"]
-        e = eager.get(s["name"])
-        e_us = f"{e['total_ms'] / e['launches'] * 1e3:8.2f}" if e else "     -  "
-        log(f"  {s['name']:12s} {s['launches']:6d} launches  avg {avg * 1e3:8.2f} us (eager {e_us} us)"
-            f"  {s['total_ms'] / total * 100:5.1f}%  {s['bytes_per_launch'] / 1e6:8.3f} MB"
-            f"  {s['bytes_per_launch'] / (avg * 1e-3) / 1e9:8.1f} GB/s")
-    dom = max(stats, key=lambda s: s["total_ms"])
-    dom_avg_s = dom["total_ms"] / dom["launches"] * 1e-3
-    achieved = dom["bytes_per_launch"] / dom_avg_s / 1e9
-    gemv = [s for s in stats if s["name"].endswith("_gemv")]
-    gemv_bytes = sum(s["bytes_per_launch"] * s["launches"] for s in gemv)
-    gemv_s = sum(s["total_ms"] for s in gemv) * 1e-3
-    m.close()
-
-    traffic = traffic_from(a.traffic_from, dom["name"]) if a.traffic_from else None
-    if traffic:
-        log(f"traffic of {dom['name']}: {traffic['fetch'] / 1e6:.3f} MB fetched + {traffic['write'] / 1e6:.3f} MB written "
-            f"per launch (counter factors {traffic['fetch_factor']:.3f} / {traffic['write_factor']:.3f})")
-    cpu = None if a.no_cpu else cpu_baseline(cfg, path, prompt, a.cpu_tokens)
-    match = None if a.no_cpu else greedy_parity(cfg, path, prompt, a.cpu_tokens, ids_gpu, gen["logits"])
-
-    out = {
-        "metric": cfg["metric"],
-        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": a.warmup,
-        "ms_per_step": round(wall / steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "int8",
-        "data": "synthetic: seeded N(0,0.02) random-init weights (" + ("Q4_0 layers, Q8_0 head" if cfg["fmt"] == "qwb"
-                 else "Q8_0 with fp32 scales") + "), seeded prompt ids",
-        "config": {"workload": cfg["workload"], "prompt_tokens": len(prompt), "decode_steps": steps,
-                   "decoding": decoding,
-                   "ctx": ctx_used, "batch": 1},
-        "roofline": {"bound": "hbm", "kernel": dom["name"], "achieved": round(achieved, 1), "peak": PEAK_HBM,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4),
-                     "traffic": round(traffic["fetch"] + traffic["write"]) if traffic else None,
-                     "avg_launch_us": round(dom_avg_s * 1e6, 3), "bytes_per_launch": round(dom["bytes_per_launch"])},
-        "gemv_all": {"achieved": round(gemv_bytes / gemv_s / 1e9, 1), "unit": "GB/s",
-                     "frac": round(gemv_bytes / gemv_s / 1e9 / PEAK_HBM, 4),
-                     "share_of_step": round(sum(s["total_ms"] for s in gemv) / total, 4)},
-        "cpu_baseline": cpu,
-        "greedy_vs_reference": match,
-    }
+        path = model_file(cfg)
+        return prefill_bench(a, cfg, path, prompt_for(cfg, path))
+    out = measure(a, a.config, steps, a.warmup, a.profile_steps, a.cpu_tokens or cfg["new"], not a.no_counters)
+    if a.config == "c3" and not a.no_c5:
+        # the 7B-shape configuration, whose GEMVs carry the HBM roofline target: a shorter record
+        c5 = measure(a, "c5", 32, 4, 8, a.cpu_tokens or 8, False)
+        for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "data"):
+            c5.pop(k, None)
+        out["c5"] = c5
     print(json.dumps(out), flush=True)
 
 

@@ -59,6 +59,7 @@ struct llm_model {
     // 1.634 -> 1.547 ms; the llama2.c 288/6L and 768/12L shapes (17 and 124 MB, MALL-resident) 3-6% slower
     // with it, so they keep the default policy.
     int weights_nt = 0;
+    int head_nt = 0; // the same choice for the head GEMV alone (LLM_HEAD_NT overrides)
     // Reference-order mode (llm_set_strict, LLM_STRICT=1): every float operation in the reference's order, so
     // logits are bitwise those of qwen.c / runq.c built with strict IEEE flags.  GEMV group products summed per
     // row in group order, RMSNorm's sum of squares as one running sum, attention by attn_strict_head, and the
@@ -178,6 +179,7 @@ hipError_t launch_head(llm_model *m, bool hist) {
     a.logits_hist = hist ? m->hist : nullptr;
     a.part_val = m->part_v;
     a.part_idx = m->part_i;
+    a.nt = m->head_nt;
     return launch_gemv(8, m->gs, m->head.sf32, PRO_NORM, EPI_ARGMAX, a, m->s_head.grid, m->st);
 }
 
@@ -514,10 +516,12 @@ int finish_setup(llm_model *m) {
     for (const Layer &ly : m->L)
         b += gemv_algo_bytes(ly.qkv.rows, I.dim, wb, m->gs, sf) + gemv_algo_bytes(I.dim, I.dim, wb, m->gs, sf) +
              gemv_algo_bytes(ly.gu.rows, I.dim, wb, m->gs, sf) + gemv_algo_bytes(I.dim, I.hidden_dim, wb, m->gs, sf);
-    b += gemv_algo_bytes(m->head.rows, I.dim, 8, m->gs, m->head.sf32);
-    m->info.gemv_bytes_per_token = b;
-    m->weights_nt = b > 0.75 * 256e6;
-    if (const char *e = getenv("LLM_WEIGHTS_NT")) m->weights_nt = atoi(e) != 0; // 0 / 1: override
+    const double head_b = gemv_algo_bytes(m->head.rows, I.dim, 8, m->gs, m->head.sf32);
+    m->info.gemv_bytes_per_token = b + head_b;
+    m->weights_nt = b + head_b > 0.75 * 256e6;
+    m->head_nt = m->weights_nt;
+    if (const char *e = getenv("LLM_WEIGHTS_NT")) m->weights_nt = m->head_nt = atoi(e) != 0; // 0 / 1: override
+    if (const char *e = getenv("LLM_HEAD_NT")) m->head_nt = atoi(e) != 0;
     return 0;
 }
 
