@@ -4,6 +4,8 @@
  *   synth bin  <out.bin> <preset> [seed]    llama2.c v2 .bin (runq): Q8_0 tensors with fp32 scales
  *   presets:  qwb: tiny, c3 (Qwen2 0.5B shape), c5 (Qwen2 7B shape)    bin: tiny, c1 (288/6L), c2 (768/12L)
  *   A preset can be overridden key by key: synth qwb out.qwb c3 7 dim=1024 layers=2 ...
+ *   head_ids=<file> (qwb): the trimmed head's token ids from a file of little-endian int32, ascending (e.g. a
+ *   set the reference ships, qwen/head_tokens_65536.npy's array); head_k becomes its length.
  *
  * Formats (kept exactly as the reference reads them):
  *   .qwb: header "<4sI10i2f" in 256 bytes (qwen.c:37-42, 216-221), every array padded to 64 bytes (qwen.c:195-199),
@@ -183,8 +185,28 @@ int main(int argc, char **argv) {
     else if (is_bin && !strcmp(p, "c2")) c = (Cfg){ 768, 2048, 12, 12, 12, 32000, 32000, 1024, 32, 1e4f, 1e-5f };
     else { fprintf(stderr, "unknown preset %s\n", p); return 1; }
     g_seed = argc > 4 ? strtoull(argv[4], NULL, 10) : 1;
-    for (int i = 5; i < argc; i++)
+    int32_t *given_ids = NULL;
+    for (int i = 5; i < argc; i++) {
+        if (!strncmp(argv[i], "head_ids=", 9)) {
+            FILE *f = fopen(argv[i] + 9, "rb");
+            long bytes = -1;
+            if (f && !fseek(f, 0, SEEK_END)) bytes = ftell(f);
+            if (!f || bytes <= 0 || bytes % 4) { fprintf(stderr, "cannot read head ids from %s\n", argv[i] + 9); return 1; }
+            rewind(f);
+            given_ids = malloc((size_t)bytes);
+            if (fread(given_ids, 1, (size_t)bytes, f) != (size_t)bytes) { fprintf(stderr, "short read of %s\n", argv[i] + 9); return 1; }
+            fclose(f);
+            c.head_k = (int)(bytes / 4);
+            continue;
+        }
         if (set_key(&c, argv[i])) { fprintf(stderr, "bad override %s\n", argv[i]); return 1; }
+    }
+    if (given_ids)
+        for (int i = 0; i < c.head_k; i++)
+            if (given_ids[i] < 0 || given_ids[i] >= c.vocab || (i && given_ids[i] <= given_ids[i - 1])) {
+                fprintf(stderr, "head id %d at %d is out of range or not ascending\n", given_ids[i], i);
+                return 1;
+            }
     if (is_bin) c.head_k = c.vocab;
     int hs = c.dim / c.heads, kv = hs * c.kv_heads, L = c.layers;
     out = fopen(argv[2], "wb");
@@ -217,7 +239,9 @@ int main(int argc, char **argv) {
         write_f32(ones, c.dim, 1); /* output_norm */
         /* head_ids: ascending; the full vocabulary when head_k == vocab, else a seeded subset without stop ids */
         int32_t *ids = malloc((size_t)c.head_k * 4);
-        if (c.head_k >= c.vocab) {
+        if (given_ids) {
+            memcpy(ids, given_ids, (size_t)c.head_k * 4);
+        } else if (c.head_k >= c.vocab) {
             c.head_k = c.vocab;
             for (int i = 0; i < c.vocab; i++) ids[i] = i;
         } else {
