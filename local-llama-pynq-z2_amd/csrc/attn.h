@@ -176,19 +176,7 @@ __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc
     for (int w = 0; w < nw; w++) mx = fmaxf(mx, sred[w]);
     for (int t = tid; t < P; t += nt) sc[t] = ref_expf(sc[t] - mx);
     __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 8 <= P; t += 8) {
-            float e[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) e[u] = sc[t + u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) sum += e[u];
-        }
-        for (; t < P; t++) sum += sc[t];
-        sred[nw] = sum;
-    }
+    if (tid == 0) sred[nw] = seq_sum(sc, P);
     __syncthreads();
     const float sum = sred[nw];
     for (int t = tid; t < P; t += nt) sc[t] = sc[t] / sum;

@@ -448,12 +448,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         KERNEL_MARK(5);
         if (a.ord) { // every group product is in LDS: one thread per row adds them in group order
             __syncthreads();
-            if (tid < rows_it) {
-                const float *pr = sprod + tid * ngs;
-                float v = 0.0f;
-                for (int g = 0; g < W.ng; g++) v += pr[g];
-                srow[tid] = v;
-            }
+            if (tid < rows_it) srow[tid] = seq_sum(sprod + tid * ngs, W.ng);
         } else {
             acc = wave_sum_from(acc, rb); // lanes holding the same row
             if (lane < rb) sred[wave * rb + lane] = acc;
@@ -854,8 +849,9 @@ hipError_t launch_attention_strict(const AttnArgs &a, hipStream_t st) {
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv;
+    // at most 64 slices: the partial buffers and the o projection's merge (PRO_ATTN) hold that many per head
     if (a.hs % 4 || a.hs > 128 || ((uintptr_t)a.q & 15) || ((uintptr_t)a.kc & 15) || ((uintptr_t)a.vc & 15) ||
-        (a.kv_dim % 4) || a.splits < 1 || a.max_pos < 1)
+        (a.kv_dim % 4) || a.splits < 1 || a.splits > 64 || a.max_pos < 1)
         return hipErrorInvalidValue;
     // longest slice over every position the cache holds: ceil(P / S) with S = min(splits, ceil(P / ATT_SUB))
     const int longest = std::max(ATT_SUB, (a.max_pos + a.splits - 1) / a.splits);
