@@ -146,9 +146,10 @@ int mvh_sample(const float *logits, int n, int count, float temperature, float t
                int *rows);
 /* the prefill GEMM on caller data: y[m][r] for M tokens, weights in the reference layout (qwen planes: bits 4
  * or 8 with fp16 scales, group 32; runq: bits 0 = int8 with fp32 scales, group gs), tiled with row-blocks of
- * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d] */
+ * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d].  shape: 0 the library's choice, 10 TA + TB
+ * one wave per 16 TA rows x 16 TB tokens (TA 1 or 2, TB 1, 2 or 4) */
 int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
-                     int bits, int gs, int rb, float *y);
+                     int bits, int gs, int rb, int shape, float *y);
 /* mvh_sample with no device allocation: no counterpart in the reference; for callers that cannot allocate
  * device memory (tight serving loops, harnesses that forbid hipMalloc).  Same arguments, draws and RNG state as
  * mvh_sample, but every device buffer lives in a fixed array inside the library (about 9 MiB per GPU, held

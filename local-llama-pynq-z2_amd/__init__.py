@@ -79,7 +79,7 @@ def lib():
     L.llm_read_state.argtypes = [vp, i32, i32, vp, sz]
     L.mvh_quantize.argtypes = [vp, i32, i32, i32, vp, vp]
     L.mvh_group_dots.argtypes = [vp, vp, i32, i32, i32, i32, vp]
-    L.mvh_prefill_gemm.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp]
+    L.mvh_prefill_gemm.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp]
     L.llm_set_prefill.argtypes = [vp, i32]
     L.llm_set_sampler.argtypes = [vp, C.c_float, C.c_float, C.c_ulonglong]
     L.llm_sampler_state.argtypes = [vp, C.POINTER(C.c_ulonglong)]
@@ -119,15 +119,16 @@ def group_dots(w, xq, n, d, bits, gs=32):
     return out
 
 
-def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16):
+def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16, shape=0):
     """The prefill GEMM (int8 MFMA) on caller data: [M, d] float32.  bits 4/8: qwen planes with fp16 scales;
-    bits 0: runq int8 with fp32 scales, group gs."""
+    bits 0: runq int8 with fp32 scales, group gs.  shape: 0 the library's choice, 10 TA + TB one wave per
+    16 TA rows x 16 TB tokens (TA 1, 2; TB 1, 2, 4)."""
     w = np.ascontiguousarray(w).view(np.uint8)
     ws = np.ascontiguousarray(ws)
     xq = np.ascontiguousarray(xq, dtype=np.int8)
     xs = np.ascontiguousarray(xs, dtype=np.float32)
     y = np.empty((M, d), np.float32)
-    if lib().mvh_prefill_gemm(_ptr(w), _ptr(ws), _ptr(xq), _ptr(xs), M, n, d, bits, gs, rb, _ptr(y)) != 0:
+    if lib().mvh_prefill_gemm(_ptr(w), _ptr(ws), _ptr(xq), _ptr(xs), M, n, d, bits, gs, rb, shape, _ptr(y)) != 0:
         raise RuntimeError("mvh_prefill_gemm failed")
     return y
 

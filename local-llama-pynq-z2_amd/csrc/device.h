@@ -151,24 +151,35 @@ __device__ __forceinline__ float seq_sum(const float *p, int n) {
     return v;
 }
 
-// Quantize n floats held in LDS (`v`, 16-byte aligned) into int8 `q` (4-byte aligned) and fp32 scales `s`
-// (LDS or global), groups of gs (32 or 64; n a multiple of gs), by the whole block.  Each lane takes 4
-// consecutive values, so a group is gs/4 = 8 or 16 lanes of one DPP row and its max is max8 / max16.
+// The int8 codes of 4 consecutive values x of a group of gs values (32 or 64) spread over gs/4 lanes of one
+// DPP row, packed little-endian, and the group's scale.  Every lane of the wave calls it (the group max is
+// max8 / max16 across lanes).
+__device__ __forceinline__ uint32_t quantize_pack(float4 x, int gs, int flavor, float *scale_out) {
+    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    m = gs == 64 ? max16(m) : max8(m);
+    const float scale = quant_scale(m, flavor), inv = quant_inv(scale);
+    const uint32_t b0 = (uint8_t)quant_one(x.x, scale, inv, flavor);
+    const uint32_t b1 = (uint8_t)quant_one(x.y, scale, inv, flavor);
+    const uint32_t b2 = (uint8_t)quant_one(x.z, scale, inv, flavor);
+    const uint32_t b3 = (uint8_t)quant_one(x.w, scale, inv, flavor);
+    *scale_out = scale;
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
 // Quantize the 4 consecutive values x of vector slot i (group of gs values = gs/4 lanes of one DPP row; every
 // lane of the wave calls it, `ok` marks the lanes whose slot exists, whole groups are in or out).
 __device__ __forceinline__ void quantize_slot(float4 x, int i, bool ok, int gs, int flavor, int8_t *q, float *s) {
-    float m = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-    m = gs == 64 ? max16(m) : max8(m);
+    float scale;
+    const uint32_t packed = quantize_pack(x, gs, flavor, &scale);
     if (ok) {
-        const float scale = quant_scale(m, flavor), inv = quant_inv(scale);
-        const uint32_t b0 = (uint8_t)quant_one(x.x, scale, inv, flavor);
-        const uint32_t b1 = (uint8_t)quant_one(x.y, scale, inv, flavor);
-        const uint32_t b2 = (uint8_t)quant_one(x.z, scale, inv, flavor);
-        const uint32_t b3 = (uint8_t)quant_one(x.w, scale, inv, flavor);
-        ((uint32_t *)q)[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        ((uint32_t *)q)[i] = packed;
         if ((i & (gs / 4 - 1)) == 0) s[i / (gs / 4)] = scale;
     }
 }
+
+// Quantize n floats held in LDS (`v`, 16-byte aligned) into int8 `q` (4-byte aligned) and fp32 scales `s`
+// (LDS or global), groups of gs (32 or 64; n a multiple of gs), by the whole block.  Each lane takes 4
+// consecutive values, so a group is gs/4 = 8 or 16 lanes of one DPP row and its max is max8 / max16.
 
 __device__ __forceinline__ void block_quantize(const float *v, int n, int gs, int flavor, int8_t *q, float *s) {
     const int nq = n / 4;

@@ -89,12 +89,15 @@ extern "C" int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, 
 }
 
 extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n,
-                                int d, int bits, int gs, int rb, float *y) {
+                                int d, int bits, int gs, int rb, int shape, float *y) {
     const int wbits = bits == 0 ? 8 : bits, sf32 = bits == 0;
     if (!w || !ws || !xq || !xs || !y || M < 1 || n <= 0 || d <= 0 || d % 4 || n % 16 ||
         (bits != 0 && bits != 4 && bits != 8) || (gs != 32 && gs != 64) || (bits != 0 && gs != 32) || n % gs ||
-        (rb != 8 && rb != 16 && rb != 64)) {
-        fprintf(stderr, "mvh_prefill_gemm: bad arguments (M=%d n=%d d=%d bits=%d gs=%d rb=%d)\n", M, n, d, bits, gs, rb);
+        (rb != 8 && rb != 16 && rb != 64) ||
+        (shape != 0 && shape != 11 && shape != 12 && shape != 14 && shape != 21 && shape != 22 && shape != 24 &&
+         shape != 41 && shape != 42)) {
+        fprintf(stderr, "mvh_prefill_gemm: bad arguments (M=%d n=%d d=%d bits=%d gs=%d rb=%d shape=%d)\n", M, n, d,
+                bits, gs, rb, shape);
         return -1;
     }
     if (hook_device("mvh_prefill_gemm")) return -1;
@@ -107,15 +110,24 @@ extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *
     int *dmap = nullptr;
     std::vector<int> map(d);
     for (int i = 0; i < d; i++) map[i] = i;
+    // the caller's row-major activations in the GEMM's token-block tiles (padding tokens zero)
+    const int MB = pf_blocks(M);
+    const size_t abytes = pf_act_bytes(n, M), sfl = pf_scale_floats(ng, M);
+    std::vector<int8_t> xt(abytes, 0);
+    std::vector<float> st(sfl, 0.0f);
+    for (int m = 0; m < M; m++) {
+        for (int k = 0; k < n; k++) xt[pf_act_off(m, k, MB)] = xq[(size_t)m * n + k];
+        for (int g = 0; g < ng; g++) st[pf_scale_off(m, g, MB)] = xs[(size_t)m * ng + g];
+    }
     int rc = -1;
     if (hipMalloc(&dw, wbytes) == hipSuccess && hipMalloc(&dsc, sbytes) == hipSuccess &&
-        hipMalloc(&dt, T.bytes) == hipSuccess && hipMalloc(&dx, (size_t)M * n) == hipSuccess &&
-        hipMalloc(&dxs, (size_t)M * ng * 4) == hipSuccess && hipMalloc(&dy, (size_t)M * d * 4) == hipSuccess &&
+        hipMalloc(&dt, T.bytes) == hipSuccess && hipMalloc(&dx, abytes) == hipSuccess &&
+        hipMalloc(&dxs, sfl * 4) == hipSuccess && hipMalloc(&dy, (size_t)M * d * 4) == hipSuccess &&
         hipMalloc(&dmap, (size_t)d * 4) == hipSuccess &&
         hipMemcpy(dw, w, wbytes, hipMemcpyHostToDevice) == hipSuccess &&
         hipMemcpy(dsc, ws, sbytes, hipMemcpyHostToDevice) == hipSuccess &&
-        hipMemcpy(dx, xq, (size_t)M * n, hipMemcpyHostToDevice) == hipSuccess &&
-        hipMemcpy(dxs, xs, (size_t)M * ng * 4, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dx, xt.data(), abytes, hipMemcpyHostToDevice) == hipSuccess &&
+        hipMemcpy(dxs, st.data(), sfl * 4, hipMemcpyHostToDevice) == hipSuccess &&
         hipMemcpy(dmap, map.data(), (size_t)d * 4, hipMemcpyHostToDevice) == hipSuccess) {
         T.data = dt;
         RepackArgs ra;
@@ -131,6 +143,10 @@ extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *
         g.xs = dxs;
         g.y = dy;
         g.M = M;
+        g.shape = shape;
+        int dev = 0;
+        hipGetDevice(&dev);
+        g.simds = 4 * hip_cu_count(dev);
         if (launch_repack(ra, 0) == hipSuccess && launch_pgemm(wbits, gs, sf32, g, 0) == hipSuccess &&
             hipDeviceSynchronize() == hipSuccess &&
             hipMemcpy(y, dy, (size_t)M * d * 4, hipMemcpyDeviceToHost) == hipSuccess)

@@ -826,10 +826,11 @@ int prefill_alloc(llm_model *m, int M) {
                     (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
         if (p) hipFree(p);
     m->pf_cap = 0;
+    // the GEMM input in token-block tiles (rounded up to 16 tokens, whole chunk pairs and scale quads)
     if (hipMalloc(&m->pf_x, (size_t)M * dim * 4) != hipSuccess || hipMalloc(&m->pf_y, (size_t)M * rows * 4) != hipSuccess ||
         hipMalloc(&m->pf_q, (size_t)M * dim * 4) != hipSuccess ||
-        hipMalloc(&m->pf_s, (size_t)M * (wmax / m->gs) * 4) != hipSuccess ||
-        hipMalloc(&m->pf_a, (size_t)M * wmax) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess ||
+        hipMalloc(&m->pf_s, pf_scale_floats(wmax / m->gs, M) * 4) != hipSuccess ||
+        hipMalloc(&m->pf_a, pf_act_bytes(wmax, M)) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess ||
         hipMalloc(&m->pf_ml, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * 2 * 4) != hipSuccess ||
         hipMalloc(&m->pf_acc, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * m->hs * 4) != hipSuccess) {
         fprintf(stderr, "llm_prefill: cannot allocate the activations of %d tokens\n", M);
@@ -882,6 +883,7 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     g.xs = m->pf_s;
     g.y = m->pf_y;
     g.M = M;
+    g.simds = 4 * hip_cu_count(m->device);
     for (int l = 0; l < I.n_layers; l++) {
         const Layer &Ly = m->L[l];
         pa.kc = m->kc + (size_t)l * m->ctx * kv;

@@ -14,183 +14,396 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-// K groups of each wave of the prefill GEMM whose loads are in flight at once (one per chunk).  Residency
-// matters more than depth here: 2 stages and 1 product buffer (below) measured 14% faster on the 512-token
-// gate/up GEMM than 4 stages and 2 buffers, which hold twice the registers and LDS per block.
-#ifndef PF_STAGES
-#define PF_STAGES 2
-#endif
-// product buffers of the prefill GEMM: 2 lets a chunk's sum overlap the next chunk's products (one barrier
-// per chunk); 1 halves the LDS of a block (a second barrier per chunk) so more blocks stay resident
-#ifndef PF_PBUF
-#define PF_PBUF 1
-#endif
+// block_quantize into the token-block tiles of the next GEMM's input (token m of MB blocks)
+__device__ __forceinline__ void block_quantize_tiles(const float *v, int n, int gs, int flavor, int8_t *q, float *s,
+                                                     int m, int MB) {
+    const int nq = n / 4;
+    for (int i0 = 0; i0 < nq; i0 += blockDim.x) {
+        const int i = i0 + threadIdx.x;
+        const bool ok = i < nq; // whole groups are in or out: nq is a multiple of gs / 4
+        float scale;
+        const uint32_t packed = quantize_pack(((const float4 *)v)[ok ? i : 0], gs, flavor, &scale);
+        if (ok) {
+            *(uint32_t *)(q + pf_act_off(m, 4 * i, MB)) = packed;
+            if ((i & (gs / 4 - 1)) == 0) s[pf_scale_off(m, i / (gs / 4), MB)] = scale;
+        }
+    }
+}
 
 // ------------------------------------------------------------------------------------------------------
 // GEMM: y[m][r] = sum_g ((float)ival(r, m, g) * ws[r][g]) * xs[m][g], groups in order.
 //
-// One block of PF_KW = 4 waves per 32 rows x 32 tokens.  The K groups are dealt round-robin over the waves:
-// in chunk c wave w takes group 4c + w, runs its MFMA and forms the group's 16 products per lane; the
-// products go through LDS and each thread adds, for its 4 outputs, the chunk's 4 products in group order.
-// The sum is therefore the sequential one, while the MFMA, unpacking and product work is spread over the
-// four SIMDs of a CU (a single wave per tile leaves the down projection's 152 groups on one SIMD).
+// One wave per tile of 16 TA rows x 16 TB tokens: the wave runs all K groups of its tile in order and keeps its
+// 4 TA TB sums in registers, so no product crosses waves and no barrier is needed.
 //
-// Lane layout of one MFMA: A (rows x K): lane l holds row l%32, K = 16 (l/32) .. +16; B (K x tokens): token
-// l%32, same K half; D: token l%32, rows 8i + 4 (l/32) + j in d[4i + j].  int4 weights enter as 16 * q (the
-// nibble at the top of its byte, as in the GEMV), so D holds 16 * ival; their fp16 scales are taken as
-// ws / 16, an exact power-of-two step, and (16 ival) * (ws / 16) rounds to the same float as ival * ws.
-// Thread (w, l) owns the outputs of slot i = w: token l%32, rows 8w + 4 (l/32) .. +3.
+// Per group and 32-element chunk, TA x TB v_mfma_i32_16x16x32_i8.  Lane l = 16 j + t holds row t of A and
+// token t of B, 8 elements of the chunk each: 4 j .. 4 j + 3 and 16 + 4 j .. 16 + 4 j + 3 (the int32 sum
+// does not depend on how K is split over the lanes, only that A and B split it alike); D: token t, rows
+// 4 j .. 4 j + 3.  In the tiled weight records those elements are dword j of a row's int4 segment (low and
+// high nibbles) or of its two int8 pieces, so:
 //
-// Blocks are laid out so that all token tiles of one row tile run on the same XCD (block b goes to XCD b % 8):
-// each weight tile is read from HBM once and served from that XCD's L2 to its other token tiles.
-#define PF_KW 4
+//  - A: one 16-byte load per lane fetches whole segments, lane row r (16 lanes) taking the segment of (row
+//    block r % TA, group r / TA of the load) for its 16 rows; a 4 x 4 transpose of those dwords across the
+//    lane rows (v_permlane32_swap, v_permlane16_swap) leaves on lane row j dword j of all four segments.  int4
+//    nibbles enter as 16 q (moved to the top of their bytes), with the scale divided by 16: 16 s * (ws / 16)
+//    rounds like s * ws.
+//  - B: one 16-byte load per lane and token block brings two chunks (the input layout of pf_act_off).
+//  - activation scales: one float4 per lane and token block for 4 groups (pf_scale_off).
+//  - weight scales: each lane loads and converts TA of the 64 TA (row, group) scales of 4 groups, and they
+//    reach the lanes that apply them through the wave's LDS slots.
+//
+// With fp16 scales every group's MFMA starts from PG_MAGIC_I instead of 0, so the bits of a result are the
+// float PG_MAGIC + s exactly (s = the group's int32 sum, |s| <= 2^19 < 2^22).  With ws the row's scale and
+// nc = -PG_MAGIC * ws, which is exact (1.5 * 2^23 times an fp16 value needs 13 significant bits),
+// fmaf(PG_MAGIC + s, ws, nc) = RN(s * ws): the reference's ((float)ival) * ws (qwen.c:452) in one
+// instruction, bitwise, for finite scales.  Then p * xs and the add in group order: 3 VALU instructions per
+// output and group.  fp32 scales (3 ws is not always a float) take a conversion instead.
+//
+// The loads of the next 4 groups are in flight while the current 4 run; group g's MFMAs are issued before
+// group g - 1's products, whose sums they do not touch.  Block = 4 waves = 4 consecutive token tiles of one
+// row tile (they read the same weights); a row tile's token tiles run on one XCD (block b goes to XCD b % 8),
+// where its weights stay in L2.
+#define PG_MAGIC_I 0x4B400000
+#define PG_MAGIC 12582912.0f
+#define PG_RSRC3 0x00020000 // buffer resource word 3 for gfx9: 32-bit data format, raw (no swizzle, no stride)
 
-template <int WB, int GSZ, int SF32>
-__global__ void __launch_bounds__(64 * PF_KW) k_pgemm(PgemmArgs a) {
-    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2, KC = GSZ / 32, KW = PF_KW;
+// 4 x 4 transpose of dwords across the 4 lane rows: on entry lane row r holds x[0..3] of its own segment; on
+// return lane row j holds in x[i] dword j of lane row i's segment.
+__device__ __forceinline__ void lane_row_transpose(uint32_t (&x)[4]) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false); // x0 rows 2,3 <-> x2 rows 0,1
+    const auto s13 = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+    const auto s01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false); // odd rows <-> even rows
+    const auto s23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+    x[0] = s01[0];
+    x[1] = s01[1];
+    x[2] = s23[0];
+    x[3] = s23[1];
+}
+
+template <int WB, int GSZ, int SF32, int TA, int TB>
+__global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
+    constexpr int KC = GSZ / 32;             // 32-element chunks per group
+    constexpr int AP = WB == 4 ? 1 : 2 * KC; // 16-byte pieces per (row, group) weight segment
+    constexpr int GA = 4 / TA;               // groups per A load
+    constexpr int NAL = TA;                  // A loads per piece and 4 groups
+    constexpr int NBL = 2 * KC;              // B loads per token block and 4 groups (chunk pairs)
+    constexpr int NB = 2;                    // steps of loads in flight
+    constexpr int SB = GSZ * WB / 8, SCB = SF32 ? 4 : 2;
+    static_assert(TA == 1 || TA == 2 || TA == 4, "row blocks per tile");
     const TiledMat &W = a.W;
-    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
-    // block -> (row tile, token tile): XCD j = b % 8 takes row tiles j, j + 8, ...
+    const int xt = (W.rows + 16 * TA - 1) / (16 * TA), yt = (a.M + 16 * TB - 1) / (16 * TB), y4 = (yt + 3) / 4;
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
-    const int tx = xcd + 8 * (idx / yt), ty = idx - (idx / yt) * yt;
-    if (tx >= xt) return; // the whole block
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, h = l >> 5, rl = l & 31;
-    const int r0 = tx * 32, m0 = ty * 32;
-    const int rb = W.rb, gpc = WAVE / rb, n = W.n, ng = W.ng;
-    const int tok = min(m0 + rl, a.M - 1);
-    const int rowA = min(r0 + rl, W.rows - 1), bA = rowA / rb, laneA = rowA - bA * rb;
-    // per wave: the converted scales of the tile's 32 rows for its current group (lanes rl convert row rl,
-    // every lane reads rows 8i + 4h .. +3); per chunk (two buffers): every wave's products, [wave][i][lane]
-    __shared__ __align__(16) float s_sc[KW][32];
-    __shared__ __align__(16) float4 s_p[PF_PBUF][KW][4][WAVE];
-    const int8_t *xrow = a.xq + (size_t)tok * n + 16 * h;
-    const float *xsrow = a.xs + (size_t)tok * ng;
-    const int nib_shift = h ? 0 : 4; // int4: lanes of the low K half take the low nibbles, moved to the top
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tx = xcd + 8 * (idx / y4), ty = 4 * (idx - (idx / y4) * y4) + w;
+    if (tx >= xt || ty >= yt) return; // the whole wave (the waves of a block share nothing but the block)
+    const int l = threadIdx.x & 63, q = l >> 4, c16 = l & 15;
+    const int r0 = tx * 16 * TA, m0 = ty * 16 * TB, MB = (a.M + 15) >> 4;
+    const int rb = W.rb, ng = W.ng, gpc = WAVE / rb, lg = 31 - __builtin_clz(gpc);
+    const int nq = (ng + 3) >> 2, nfull = ng >> 2; // 4-group steps, the full ones
+    const uint32_t rstride = (uint32_t)W.nchunks * (uint32_t)W.rec;
 
-    // A ring of PF_STAGES of this wave's groups in flight.  A stage holds raw loaded words only: the int4
-    // unpacking and the scale conversion happen when the group is used, so issuing a stage never waits.
-    constexpr int NS = PF_STAGES;
-    uint4 wr[NS][KC]; // int4: the lane's 16-byte segment; int8: the K-half piece
-    v4i bv[NS][KC];
-    using ScaleBits = typename std::conditional<SF32 != 0, uint32_t, uint16_t>::type;
-    ScaleBits sr[NS]; // raw scale of the lane's A row
-    float xs[NS];
-    auto load = [&](int g, int st) {
-        const int c = g / gpc, gi = g - c * gpc;
-        const uint8_t *recA = W.data + ((size_t)bA * W.nchunks + c) * W.rec;
+    // Per-lane parts of the load offsets.  A record offset is (row block, chunk c, slot gi) -> b * rstride
+    // + c * rec + ...; for the 4 groups g0 .. g0 + 3 of a step (g0 a multiple of 4) the chunk and slot of
+    // group g0 + e split into a part common to the wave (c0 = g0 >> lg, gi0 = g0 & (gpc - 1)) and a per-lane
+    // part (e >> lg, e & (gpc - 1)), since gpc is 1, 2, 4 or 8.  Rows past the matrix clamp to its last row.
+    uint32_t offA[NAL], offS[TA];
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) {
-            if constexpr (WB == 4) wr[st][kc] = *(const uint4 *)(recA + (size_t)(gi * rb + laneA) * 16);
-            else wr[st][kc] = *(const uint4 *)(recA + (size_t)(2 * kc + h) * 1024 + (size_t)(gi * rb + laneA) * 16);
-        }
-        const uint8_t *sp = recA + 64 * SB + (size_t)(gi * rb + laneA) * SCB;
-        sr[st] = *(const ScaleBits *)sp;
+    for (int s = 0; s < NAL; s++) {
+        const int e = s * GA + q / TA; // group of this lane row within the step
+        const int row = min(r0 + 16 * (q % TA) + c16, W.rows - 1), bA = row / rb, la = row - bA * rb;
+        offA[s] = bA * rstride + (e >> lg) * (uint32_t)W.rec + ((e & (gpc - 1)) * rb + la) * 16;
+    }
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) bv[st][kc] = *(const v4i *)(xrow + (size_t)g * GSZ + 32 * kc);
-        xs[st] = xsrow[g];
-    };
-    // the products of stage st into s_p[buf][w]
-    auto products = [&](int st, int buf) {
-        v16i d = v16i{};
+    for (int t = 0; t < TA; t++) {
+        const int ent = 64 * t + l, e = ent / (16 * TA), rho = ent - e * 16 * TA;
+        const int row = min(r0 + rho, W.rows - 1), bS = row / rb, la = row - bS * rb;
+        offS[t] = bS * rstride + (e >> lg) * (uint32_t)W.rec + 64 * SB + ((e & (gpc - 1)) * rb + la) * SCB;
+    }
+    uint32_t offB[TB], offX[TB];
 #pragma unroll
-        for (int kc = 0; kc < KC; kc++) {
-            v4i av;
-            if constexpr (WB == 4) {
-                const uint4 q = wr[st][kc];
-                const uint32_t m = 0xF0F0F0F0u;
-                av = v4i{(int)((q.x << nib_shift) & m), (int)((q.y << nib_shift) & m), (int)((q.z << nib_shift) & m),
-                         (int)((q.w << nib_shift) & m)};
-            } else {
-                av = v4i{(int)wr[st][kc].x, (int)wr[st][kc].y, (int)wr[st][kc].z, (int)wr[st][kc].w};
+    for (int j = 0; j < TB; j++) {
+        const int tb = min(ty * TB + j, MB - 1); // past the last token block: clamped, outputs not stored
+        offB[j] = (uint32_t)tb * 1024 + 16 * l;
+        offX[j] = (uint32_t)(16 * tb + c16) * 16;
+    }
+
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)W.data, 0, (int)W.bytes, PG_RSRC3);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.xq, 0, (int)pf_act_bytes(W.n, a.M), PG_RSRC3);
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.xs, 0, (int)(pf_scale_floats(ng, a.M) * 4), PG_RSRC3);
+
+    // the loads of two steps: the current one and the next
+    uint4 ar[NB][NAL][AP]; // raw A segments
+    uint32_t sr[NB][TA];   // raw weight scales
+    uint4 br[NB][TB][NBL]; // B chunk pairs
+    float4 xr[NB][TB];     // activation scales of the 4 groups
+    // Loads of step qs (groups 4 qs ..) into buffer k: a full step (clamp false) with offsets common to the
+    // wave, or the last step of ng % 4 groups, whose lanes clamp their groups to ng - 1 (per-lane offsets).
+    // The two kinds are separate call sites: one load sequence must not hold both (buffer loads cannot fault,
+    // so the compiler would issue both and wait between them).
+    auto load = [&](int qs, int k, bool clamp) {
+        const int g0 = 4 * qs;
+        if (!clamp) {
+            const int c0 = g0 >> lg, gi0 = g0 & (gpc - 1);
+            const int wo = c0 * (int)W.rec + gi0 * rb * 16, so = c0 * (int)W.rec + gi0 * rb * SCB;
+#pragma unroll
+            for (int s = 0; s < NAL; s++)
+#pragma unroll
+                for (int p = 0; p < AP; p++) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, offA[s] + p * 1024, wo, 0);
+                    ar[k][s][p] = make_uint4(v[0], v[1], v[2], v[3]);
+                }
+#pragma unroll
+            for (int t = 0; t < TA; t++) {
+                if constexpr (SF32) sr[k][t] = __builtin_amdgcn_raw_buffer_load_b32(rw, offS[t], so, 0);
+                else sr[k][t] = __builtin_amdgcn_raw_buffer_load_b16(rw, offS[t], so, 0);
             }
-            d = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[st][kc], d, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int s = 0; s < NAL; s++) {
+                const int g = min(g0 + s * GA + q / TA, ng - 1), c = g >> lg, gi = g & (gpc - 1);
+                const int row = min(r0 + 16 * (q % TA) + c16, W.rows - 1), bA = row / rb, la = row - bA * rb;
+                const uint32_t o = bA * rstride + c * (uint32_t)W.rec + (gi * rb + la) * 16;
+#pragma unroll
+                for (int p = 0; p < AP; p++) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b128(rw, o + p * 1024, 0, 0);
+                    ar[k][s][p] = make_uint4(v[0], v[1], v[2], v[3]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < TA; t++) {
+                const int ent = 64 * t + l, e = ent / (16 * TA), rho = ent - e * 16 * TA;
+                const int g = min(g0 + e, ng - 1), c = g >> lg, gi = g & (gpc - 1);
+                const int row = min(r0 + rho, W.rows - 1), bS = row / rb, la = row - bS * rb;
+                const uint32_t o = bS * rstride + c * (uint32_t)W.rec + 64 * SB + (gi * rb + la) * SCB;
+                if constexpr (SF32) sr[k][t] = __builtin_amdgcn_raw_buffer_load_b32(rw, o, 0, 0);
+                else sr[k][t] = __builtin_amdgcn_raw_buffer_load_b16(rw, o, 0, 0);
+            }
         }
-        // one scale conversion per lane, exchanged within the wave through its own LDS slots
-        if (h == 0)
-            s_sc[w][rl] = SF32 ? __uint_as_float(sr[st]) : f16_bits_to_f32(sr[st]) * (WB == 4 ? 0.0625f : 1.0f);
+        // chunk pairs of the step (4 KC chunks from chunk 4 KC qs), within the input's last pair
+        const int np = (ng * KC + 1) >> 1;
+#pragma unroll
+        for (int j = 0; j < TB; j++) {
+#pragma unroll
+            for (int t = 0; t < NBL; t++) {
+                const int pr = min(2 * KC * (g0 >> 2) + t, np - 1);
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rx, offB[j], pr * MB * 1024, 0);
+                br[k][j][t] = make_uint4(v[0], v[1], v[2], v[3]);
+            }
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, offX[j], (g0 >> 2) * MB * 256, 0);
+            xr[k][j] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                   __uint_as_float(v[3]));
+        }
+    };
+
+    // the step's weights after the transpose: wa[k][s][p][i] = dword q of lane row i's segment of A load s
+    uint32_t wa[NAL][AP][4];
+    __shared__ __align__(16) float s_ws[4][NB][4][16 * TA], s_nc[4][NB][4][16 * TA];
+    auto wave_sync = [] {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 ws4 = *(const float4 *)(&s_sc[w][8 * i + 4 * h]);
-            float4 p;
-            p.x = (float)d[4 * i] * ws4.x; // qwen.c:452, runq.c:452
-            p.y = (float)d[4 * i + 1] * ws4.y;
-            p.z = (float)d[4 * i + 2] * ws4.z;
-            p.w = (float)d[4 * i + 3] * ws4.w;
-            p.x = p.x * xs[st];
-            p.y = p.y * xs[st];
-            p.z = p.z * xs[st];
-            p.w = p.w * xs[st];
-            s_p[buf][w][i][l] = p;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier(); // this wave's scale reads come before its next group's scale writes
     };
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    const int nc = (ng + KW - 1) / KW; // chunks; wave w's group in chunk c is KW c + w when below ng
-    // Every stage is loaded and used, past the last group too (clamped to it; its products are not added):
-    // with no branch around the loads the compiler's count of loads in flight stays exact, so waiting for
-    // one stage does not wait for the stages issued after it.
+    // begin a step from buffer k: transpose the A segments, convert this lane's weight scales into LDS
+    // buffer k (then wave_sync before any read of it)
+    auto begin = [&](int k) {
 #pragma unroll
-    for (int st = 0; st < NS - 1; st++) load(min(KW * st + w, ng - 1), st);
-    for (int c0 = 0; c0 < nc; c0 += NS) {
+        for (int s = 0; s < NAL; s++)
 #pragma unroll
-        for (int st = 0; st < NS; st++) {
-            const int c = c0 + st;
-            if (c >= nc) break;
-            load(min(KW * (c + NS - 1) + w, ng - 1), (st + NS - 1) % NS);
-            const int buf = PF_PBUF == 2 ? (c & 1) : 0;
-            products(st, buf); // past the last group: a clamped copy that the sum below skips
-            __syncthreads();
-            const int cnt = ng - KW * c;
+            for (int p = 0; p < AP; p++) {
+                uint32_t x[4] = {ar[k][s][p].x, ar[k][s][p].y, ar[k][s][p].z, ar[k][s][p].w};
+                lane_row_transpose(x);
 #pragma unroll
-            for (int v = 0; v < KW; v++) { // the chunk's groups in order
-                if (v < cnt) {
-                    const float4 p = s_p[buf][v][w][l];
-                    acc.x = acc.x + p.x;
-                    acc.y = acc.y + p.y;
-                    acc.z = acc.z + p.z;
-                    acc.w = acc.w + p.w;
+                for (int i = 0; i < 4; i++) wa[s][p][i] = x[i];
+            }
+#pragma unroll
+        for (int t = 0; t < TA; t++) {
+            const int ent = 64 * t + l, e = ent / (16 * TA), rho = ent - e * 16 * TA;
+            const float ws = SF32 ? __uint_as_float(sr[k][t])
+                                  : f16_bits_to_f32((uint16_t)sr[k][t]) * (WB == 4 ? 0.0625f : 1.0f);
+            s_ws[w][k][e][rho] = ws;
+            s_nc[w][k][e][rho] = -(PG_MAGIC * ws);
+        }
+    };
+    const v4i c0 = SF32 ? v4i{0, 0, 0, 0} : v4i{PG_MAGIC_I, PG_MAGIC_I, PG_MAGIC_I, PG_MAGIC_I};
+    // MFMAs of group e of the step in buffer k
+    auto mfma = [&](int k, int e, v4i (&dn)[TA][TB]) {
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            const int ch = e * KC + kc; // chunk within the step: pair ch / 2, half ch % 2
+#pragma unroll
+            for (int i = 0; i < TA; i++) {
+                const int s = e / GA, li = (e % GA) * TA + i; // A load and lane row of (group e, block i)
+                uint32_t lo, hi;
+                if constexpr (WB == 4) {
+                    const uint32_t x = wa[s][0][li];
+                    lo = (x << 4) & 0xF0F0F0F0u;
+                    hi = x & 0xF0F0F0F0u;
+                } else {
+                    lo = wa[s][2 * kc][li];
+                    hi = wa[s][2 * kc + 1][li];
+                }
+                const long av = (long)(((uint64_t)hi << 32) | lo);
+#pragma unroll
+                for (int j = 0; j < TB; j++) {
+                    const uint4 &v = br[k][j][ch >> 1];
+                    const long bw = (ch & 1) ? (long)(((uint64_t)v.w << 32) | v.z) : (long)(((uint64_t)v.y << 32) | v.x);
+                    dn[i][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, kc == 0 ? c0 : dn[i][j], 0, 0, 0);
                 }
             }
-            // with two buffers no second barrier: the next chunk writes the other buffer, and the one after
-            // that writes this buffer only after the next chunk's barrier, which every thread reaches after
-            // these reads
-            if (PF_PBUF == 1) __syncthreads();
         }
+    };
+    float acc[TA][TB][4];
+#pragma unroll
+    for (int i = 0; i < TA; i++)
+#pragma unroll
+        for (int j = 0; j < TB; j++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[i][j][k] = 0.0f;
+    // the weight scales of this lane's output rows for group e of the step in buffer k, read from LDS one
+    // group ahead of their use (by group parity)
+    float4 scw[2][TA], scn[2][TA];
+    auto read_scales = [&](int k, int e) {
+#pragma unroll
+        for (int i = 0; i < TA; i++) {
+            scw[e & 1][i] = *(const float4 *)(&s_ws[w][k][e][16 * i + 4 * q]);
+            scn[e & 1][i] = *(const float4 *)(&s_nc[w][k][e][16 * i + 4 * q]);
+        }
+    };
+    // products of group e of the step in buffer k (MFMA results d, scales read by read_scales) added to the
+    // sums; x: the group's activation scales when they are not in xr[k] any more
+    auto products = [&](const v4i (&d)[TA][TB], int k, int e, const float *x) {
+#pragma unroll
+        for (int i = 0; i < TA; i++) {
+            const float4 ws4 = scw[e & 1][i], nc4 = scn[e & 1][i];
+            const float wsv[4] = {ws4.x, ws4.y, ws4.z, ws4.w}, ncv[4] = {nc4.x, nc4.y, nc4.z, nc4.w};
+#pragma unroll
+            for (int j = 0; j < TB; j++) {
+                const float xv[4] = {xr[k][j].x, xr[k][j].y, xr[k][j].z, xr[k][j].w};
+                const float xe = x ? x[j] : xv[e];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float p = SF32 ? (float)d[i][j][r] * wsv[r] : fmaf(__int_as_float(d[i][j][r]), wsv[r], ncv[r]);
+                    p = p * xe; // qwen.c:452, runq.c:452
+                    acc[i][j][r] = acc[i][j][r] + p;
+                }
+            }
+        }
+    };
+    v4i d[2][TA][TB]; // MFMA results by group parity
+    // Step qs from buffer k (k = qs & 1).  The next step's loads go first, into buffer k ^ 1 (next = 0 none,
+    // 1 a full step, 2 the last, partial step); of that buffer only the previous step's group 3 activation
+    // scales are still needed, and are kept aside.  Group e's scale reads and MFMAs precede group e - 1's
+    // products (group 0's predecessor: the previous step's group 3), so the LDS and MFMA latencies pass during
+    // VALU work.  The scheduling barrier after each group keeps that order (the compiler would otherwise
+    // hoist later groups' scale reads, holding their registers).  In the partial step groups past ng are
+    // skipped.
+    auto step = [&](int qs, int k, int next, bool last) {
+        float x3[TB];
+#pragma unroll
+        for (int j = 0; j < TB; j++) x3[j] = xr[k ^ 1][j].w;
+        if (next == 1) load(qs + 1, k ^ 1, false);
+        if (next == 2) load(qs + 1, k ^ 1, true);
+        begin(k);
+        wave_sync();
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int g = 4 * qs + e;
+            if (last && g >= ng) break;
+            read_scales(k, e);
+            mfma(k, e, d[e & 1]);
+            if (e == 0) {
+                if (qs > 0) products(d[1], k ^ 1, 3, x3);
+            } else {
+                products(d[(e - 1) & 1], k, e - 1, nullptr);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    const bool partial = nq > nfull;
+    int qs = 0;
+    if (nfull > 0) {
+        load(0, 0, false);
+        // full steps followed by full steps, two at a time (buffers 0, 1), then the last one or two full steps
+        for (; qs + 2 < nfull; qs += 2) {
+            step(qs, 0, 1, false);
+            step(qs + 1, 1, 1, false);
+        }
+        if (qs + 2 == nfull) {
+            step(qs, 0, 1, false);
+            step(qs + 1, 1, partial ? 2 : 0, false);
+        } else {
+            step(qs, 0, partial ? 2 : 0, false);
+        }
+        qs = nfull;
+    } else {
+        load(0, 0, true);
     }
-    const int m = m0 + rl, R = r0 + 8 * w + 4 * h;
-    if (m < a.M) {
-        float *dst = a.y + (size_t)m * W.rows + R;
-        if (R + 3 < W.rows) *(float4 *)dst = acc;
-        else {
-            const float v[4] = {acc.x, acc.y, acc.z, acc.w};
-            for (int j = 0; j < 4; j++)
-                if (R + j < W.rows) dst[j] = v[j];
+    if (partial) { // a last step of ng % 4 groups
+        if (qs & 1) step(qs, 1, 0, true);
+        else step(qs, 0, 0, true);
+    }
+    // the products of the last group, ng - 1: group (ng - 1) % 4 of step nq - 1, buffer (nq - 1) & 1
+    {
+        const int e = (ng - 1) & 3, k = (nq - 1) & 1;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int ee = 0; ee < 4; ee++)
+                if (kk == k && ee == e) products(d[ee & 1], kk, ee, nullptr);
+    }
+#pragma unroll
+    for (int j = 0; j < TB; j++) {
+        const int m = m0 + 16 * j + c16;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int i = 0; i < TA; i++) {
+            const int R = r0 + 16 * i + 4 * q; // rows % 4 == 0: R < rows means all four rows are
+            if (R < W.rows)
+                *(float4 *)(a.y + (size_t)m * W.rows + R) =
+                    make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         }
     }
 }
 
 hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStream_t st) {
     const TiledMat &W = a.W;
-    // rows in whole groups of 4 (scale loads), 16-byte aligned activation rows and output rows
-    if (a.M < 1 || W.rows % 4 || W.n % gs || W.n % 16 || ((uintptr_t)a.xq & 15) || ((uintptr_t)a.y & 15) ||
-        W.gs != gs || W.wbits != wbits || W.sf32 != sf32)
+    // rows in whole groups of 4 (float4 outputs), aligned input and output, int4 only with groups of 32
+    if (a.M < 1 || W.rows % 4 || W.n % gs || ((uintptr_t)a.xq & 15) || ((uintptr_t)a.xs & 15) ||
+        ((uintptr_t)a.y & 15) || W.gs != gs || W.wbits != wbits || W.sf32 != sf32 || (wbits == 4 && gs != 32))
         return hipErrorInvalidValue;
-    const int xt = (W.rows + 31) / 32, yt = (a.M + 31) / 32;
-    const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * yt);
+    // buffer loads address the matrix and the input with 31-bit sizes
+    if (W.bytes >= ((size_t)1 << 31) || pf_act_bytes(W.n, a.M) >= ((size_t)1 << 31) ||
+        pf_scale_floats(W.ng, a.M) * 4 >= ((size_t)1 << 31))
+        return hipErrorInvalidValue;
+    const int shape = a.shape ? a.shape : pgemm_pick_shape(W.rows, a.M, a.simds);
+    const int TA = shape / 10, TB = shape % 10;
+#define PGW(WB_, GS_, SF_, TA_, TB_)                                                                           \
+    if (TA == TA_ && TB == TB_) {                                                                             \
+        const int xt = (W.rows + 16 * TA_ - 1) / (16 * TA_), yt = (a.M + 16 * TB_ - 1) / (16 * TB_);          \
+        const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * ((yt + 3) / 4));                              \
+        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_, TA_, TB_>), dim3(blocks), dim3(256), 0, st, a);           \
+        return hipGetLastError();                                                                             \
+    }
 #define PG(WB_, GS_, SF_)                                                                                      \
     if (wbits == WB_ && gs == GS_ && sf32 == SF_) {                                                           \
-        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_>), dim3(blocks), dim3(64 * PF_KW), 0, st, a);                \
-        return hipGetLastError();                                                                             \
+        PGW(WB_, GS_, SF_, 1, 1)                                                                              \
+        PGW(WB_, GS_, SF_, 1, 2)                                                                              \
+        PGW(WB_, GS_, SF_, 1, 4)                                                                              \
+        PGW(WB_, GS_, SF_, 2, 1)                                                                              \
+        PGW(WB_, GS_, SF_, 2, 2)                                                                              \
+        PGW(WB_, GS_, SF_, 2, 4)                                                                              \
+        PGW(WB_, GS_, SF_, 4, 1)                                                                              \
+        PGW(WB_, GS_, SF_, 4, 2)                                                                              \
+        return hipErrorInvalidValue;                                                                          \
     }
     PG(4, 32, 0)
     PG(8, 32, 0)
     PG(8, 32, 1)
     PG(8, 64, 1)
 #undef PG
+#undef PGW
     return hipErrorInvalidValue;
 }
 
@@ -241,7 +454,7 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     ss = 1.0f / sqrtf(ss);
     for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.norm_w[i] * (ss * sv[i]);
     __syncthreads();
-    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
+    block_quantize_tiles(sv, n, a.gs, a.qflavor, a.oq, a.os, m, pf_blocks(a.M));
 }
 
 // QKV rows of token m: bias (qwen.c:521-522), RoPE at position p0 + m (qwen.c:478-488 NeoX pairs; runq.c:506-521
@@ -324,7 +537,7 @@ __global__ void __launch_bounds__(256) k_p_swiglu_quant(ProwArgs a) {
         }
     }
     __syncthreads();
-    block_quantize(sv, hid, a.gs, a.qflavor, a.oq + (size_t)m * hid, a.os + (size_t)m * (hid / a.gs));
+    block_quantize_tiles(sv, hid, a.gs, a.qflavor, a.oq, a.os, m, pf_blocks(a.M));
 }
 
 // ------------------------------------------------------------------------------------------------------
@@ -466,8 +679,7 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
         f32x4v val[DT];
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) val[dt] = o[dt] / l_tot;
-        int8_t *oq = a.oq + (size_t)m * a.dim + (size_t)h * HS + 4 * g;
-        float *os = a.os + ((size_t)m * a.dim + (size_t)h * HS) / a.gs;
+        const int MB = pf_blocks(a.M), k0 = h * HS + 4 * g; // this lane's elements k0 + 16 dt .. +3
 #pragma unroll
         for (int g0 = 0; g0 < DT; g0++) {
             if (g0 % tiles) continue; // not the first tile of a group
@@ -488,9 +700,9 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
                     const uint32_t b1 = (uint8_t)quant_one(v.y, scale, inv, a.qflavor);
                     const uint32_t b2 = (uint8_t)quant_one(v.z, scale, inv, a.qflavor);
                     const uint32_t b3 = (uint8_t)quant_one(v.w, scale, inv, a.qflavor);
-                    *(uint32_t *)(oq + 16 * (g0 + k)) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                    *(uint32_t *)(a.oq + pf_act_off(m, k0 + 16 * (g0 + k), MB)) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
                 }
-            if (mine && g == 0) os[16 * g0 / a.gs] = scale;
+            if (mine && g == 0) a.os[pf_scale_off(m, (h * HS + 16 * g0) / a.gs, MB)] = scale;
         }
         if (S_m == 1) return;
     }
@@ -581,7 +793,7 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
         row[o] = v;
     }
     __syncthreads();
-    block_quantize(row, a.dim, a.gs, a.qflavor, a.oq + (size_t)m * a.dim, a.os + (size_t)m * (a.dim / a.gs));
+    block_quantize_tiles(row, a.dim, a.gs, a.qflavor, a.oq, a.os, m, pf_blocks(a.M));
 }
 
 // Reference-order causal attention: block (h, m) is query head h of token m over positions 0 .. p0 + m
@@ -599,7 +811,7 @@ __global__ void __launch_bounds__(256) k_p_quant_rows(ProwArgs a) {
     const int m = blockIdx.x, n = a.dim;
     for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.xb[(size_t)m * n + i];
     __syncthreads();
-    block_quantize(sv, n, a.gs, a.qflavor, a.oq + (size_t)m * n, a.os + (size_t)m * (n / a.gs));
+    block_quantize_tiles(sv, n, a.gs, a.qflavor, a.oq, a.os, m, pf_blocks(a.M));
 }
 
 hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {

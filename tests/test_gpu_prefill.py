@@ -22,33 +22,65 @@ def golden(name, n):
     return np.fromfile(os.path.join(GOLDEN, f"tiny_{name}_ref.logits"), dtype="<f4").reshape(-1, n)
 
 
-@pytest.mark.parametrize("M,n,d,bits,rb", [(1, 96, 36, 4, 16), (7, 96, 36, 8, 16), (33, 896, 128, 4, 16),
-                                           (64, 896, 64, 8, 16), (40, 4864, 32, 4, 8), (5, 256, 20, 4, 16),
-                                           (70, 128, 100, 4, 8), (96, 64, 12288, 4, 16), (64, 896, 16384, 4, 16),
-                                           (64, 160, 16384, 8, 16)])
-def test_prefill_gemm_bit_exact_qwen(M, n, d, bits, rb):
-    """group counts below, at and above the 4 waves the K groups are dealt over; grids of 1024 tiles and more"""
-    rng = np.random.default_rng(100 + M + n + d + bits)
-    w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
-    s = f16_scales(rng, d * n // 32)
-    xq = rng.integers(-128, 128, size=(M, n), dtype=np.int8)
-    xs = rng.uniform(1e-3, 1e-1, size=(M, n // 32)).astype(np.float32)
-    y = pkg().prefill_gemm(w, s, xq, xs, M, n, d, bits, 32, rb)
+# 0: the library's choice; 10 TA + TB: one wave per 16 TA rows x 16 TB tokens
+SHAPES = [0, 11, 12, 14, 21, 22, 24, 41, 42]
+
+
+def check_qwen_gemm(w, s, xq, xs, M, n, d, bits, rb, shape):
+    y = pkg().prefill_gemm(w, s, xq, xs, M, n, d, bits, 32, rb, shape)
     for m in range(M):
         o = np.empty(d, np.float32)
         oracle().or_matvec4(ptr(o), ptr(w), ptr(s), ptr(xq[m]), ptr(xs[m]), n, d, bits)
         assert np.array_equal(y[m].view(np.uint32), o.view(np.uint32)), m
 
 
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("M,n,d,bits,rb", [(1, 96, 36, 4, 16), (7, 96, 36, 8, 16), (33, 896, 128, 4, 16),
+                                           (64, 896, 64, 8, 16), (40, 4864, 32, 4, 8), (5, 256, 20, 4, 16),
+                                           (70, 128, 100, 4, 8), (96, 64, 12288, 4, 16), (64, 896, 16384, 4, 16),
+                                           (64, 160, 16384, 8, 16)])
+def test_prefill_gemm_bit_exact_qwen(M, n, d, bits, rb, shape):
+    """group counts below, at and above the 4 waves the K groups are dealt over; grids of 1024 tiles and more;
+    rows and tokens that fill no tile, one tile, or end inside one"""
+    rng = np.random.default_rng(100 + M + n + d + bits)
+    w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
+    s = f16_scales(rng, d * n // 32)
+    xq = rng.integers(-128, 128, size=(M, n), dtype=np.int8)
+    xs = rng.uniform(1e-3, 1e-1, size=(M, n // 32)).astype(np.float32)
+    check_qwen_gemm(w, s, xq, xs, M, n, d, bits, rb, shape)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("bits", [4, 8])
+def test_prefill_gemm_bit_exact_special_scales(bits, shape):
+    """fp16 scales of every exponent field (zero, subnormals, up to 65504) and both signs, row by row; the
+    extreme int8 activations and weights (every group sum at its largest magnitude in some rows): the
+    one-instruction product with the biased MFMA start must round like ((float)ival) * ws for all of them"""
+    M, n, d = 40, 256, 64
+    rng = np.random.default_rng(7 + bits)
+    w = rng.integers(0, 256, size=d * n * bits // 8, dtype=np.uint8)
+    if bits == 4:
+        w.reshape(d, n // 2)[:8] = 0x88        # int4 -8 everywhere
+    else:
+        w.reshape(d, n)[:8] = 0x80             # int8 -128 everywhere
+    s = f16_scales(rng, d * n // 32, special_rows=1, ng=n // 32)
+    xq = rng.integers(-128, 128, size=(M, n), dtype=np.int8)
+    xq[:4] = -128
+    xq[4:8] = 127
+    xs = rng.uniform(1e-3, 1e-1, size=(M, n // 32)).astype(np.float32)
+    check_qwen_gemm(w, s, xq, xs, M, n, d, bits, 16, shape)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("M,n,d,gs,rb", [(9, 288, 32, 32, 64), (33, 768, 96, 64, 64), (17, 768, 64, 32, 16),
                                          (64, 288, 16384, 32, 64), (64, 192, 16384, 64, 64)])
-def test_prefill_gemm_bit_exact_runq(M, n, d, gs, rb):
+def test_prefill_gemm_bit_exact_runq(M, n, d, gs, rb, shape):
     rng = np.random.default_rng(200 + M + n + d + gs)
     wq = rng.integers(-128, 128, size=d * n, dtype=np.int8)
     ws = rng.uniform(1e-4, 2e-2, size=d * n // gs).astype(np.float32)
     xq = rng.integers(-128, 128, size=(M, n), dtype=np.int8)
     xs = rng.uniform(1e-3, 1e-1, size=(M, n // gs)).astype(np.float32)
-    y = pkg().prefill_gemm(wq, ws, xq, xs, M, n, d, 0, gs, rb)
+    y = pkg().prefill_gemm(wq, ws, xq, xs, M, n, d, 0, gs, rb, shape)
     for m in range(M):
         o = np.empty(d, np.float32)
         oracle().or_matvec_runq(ptr(o), ptr(wq), ptr(ws), ptr(xq[m]), ptr(xs[m]), n, d, gs)
