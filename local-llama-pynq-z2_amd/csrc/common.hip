@@ -25,7 +25,6 @@ static void gemv_split(GemvShape &s, int C, int per_wave, const TiledMat &T, int
 }
 
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus) {
-    (void)pro;
     GemvShape s;
     const int C = T.nchunks;
     if (cus < 1) cus = 1;
@@ -50,13 +49,16 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     int resident = cus * (waves < 16 ? 16 / waves : 1);
     if (iters > resident) {
         if (!ordered) {
-            gemv_split(s, C, 16, T, epi);
+            // streaming split: about 16 chunks per wave; the SwiGLU epilogue's blocks (4 row-blocks, 32 hidden
+            // values) measured fastest with one wave per row-block reading all of its chunks
+            gemv_split(s, C, epi == EPI_SWIGLU ? C : 16, T, epi);
             if (s.ord && (size_t)s.nb * T.rb * (T.ng + 1) * 4 > 65536) s.nb = 1; // keep the products in LDS
             iters = (T.nblocks + s.nb - 1) / s.nb;
             waves = s.kw * s.nb;
             resident = cus * (waves < 16 ? 16 / waves : 1);
         }
-        s.grid = iters > resident ? resident : iters;
+        // the head's argmax runs a persistent grid; every other GEMV one block per iteration
+        s.grid = epi == EPI_ARGMAX && iters > resident ? resident : iters;
     } else {
         // latency shape: when the iterations outnumber the CUs, some CUs hold two blocks and finish last;
         // more row-blocks per iteration (more waves per block) keep it at one block per CU (a wider rule that
@@ -68,6 +70,10 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
         }
         s.grid = iters;
     }
+    // The attention merge gives each thread one 4-value slot of the input: a block covers the whole input
+    // in one pass (a second pass would read its operands after the weights are issued).
+    if (pro == PRO_ATTN)
+        while (s.kw * s.nb * 64 < T.n / 4 && s.kw * s.nb < 16 && s.kw < C) s.kw++;
     if (s.grid < 1) s.grid = 1;
     s.depth = 2;
     return s;

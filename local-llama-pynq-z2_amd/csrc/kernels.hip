@@ -71,6 +71,9 @@ struct Fmt {
     static constexpr int PIECES = SB / 16;
     static constexpr int SCB = SF32 ? 4 : 2;
     static constexpr int UNROLL = 4 / PIECES;
+    // a scale as loaded: fp32 bits, or the fp16 scales of the lane pair (lane & ~1, lane | 1) as one dword,
+    // split at use (a 16-bit load would be widened right after it, making the compiler wait for it there)
+    using ST = uint32_t;
 };
 
 __device__ __forceinline__ float rope_pair_out(float self, float partner, bool first, float c, float s) {
@@ -92,25 +95,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const TiledMat &W)
 
 // Cache policy of the weight loads (the buffer load's cache-policy operand): 0, or 2 = non-temporal (`nt`).
 // GemvArgs::nt selects non-temporal loads when a decode step streams more weights than the MALL keeps.
+//
+// A buffer load whose lane offset is at or past the resource's size returns zeros without touching memory.
+// Loads with nothing to read (a chunk past the row-block's end, a batch past the wave's stream) take this
+// offset, so every call issues the same instructions: the compiler then knows exactly how many loads are in
+// flight when a batch is used, and waits for that batch alone instead of draining the ones behind it.
+#define OOB_OFFSET 0x80000000u
 template <int WB, int GSZ, int SF32, int POLICY>
 __device__ __forceinline__ void load_batch(__amdgpu_buffer_rsrc_t rs, uint32_t rb_off, uint32_t rec_bytes, int nchunks,
-                                           int c0, int kw, int lane,
+                                           int c0, int kw, int lane, bool live,
                                            uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
-                                           uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+                                           typename Fmt<WB, GSZ, SF32>::ST (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
     using F = Fmt<WB, GSZ, SF32>;
-    // Every load is issued: a chunk index past the end reads the row-block's last record, which use_batch
-    // then skips.  Unconditional loads keep the wave from waiting for them at a branch merge.
 #pragma unroll
     for (int u = 0; u < F::UNROLL; u++) {
+        const bool ok = live && c0 + u * kw < nchunks;
         const uint32_t soff = rb_off + (uint32_t)min(c0 + u * kw, nchunks - 1) * rec_bytes;
 #pragma unroll
         for (int p = 0; p < F::PIECES; p++) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16 + p * 1024, soff, POLICY);
+            const uint32_t voff = ok ? (uint32_t)(lane * 16 + p * 1024) : OOB_OFFSET;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)voff, soff, POLICY);
             wv[u][p] = *(const uint4 *)&v;
         }
-        if constexpr (SF32) sr[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 64 * F::SB + lane * 4, soff, POLICY);
-        else sr[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 64 * F::SB + lane * 2, soff, POLICY);
+        const uint32_t voff_s = ok ? (uint32_t)(64 * F::SB + (SF32 ? lane * 4 : (lane & ~1) * 2)) : OOB_OFFSET;
+        sr[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)voff_s, soff, POLICY);
     }
+}
+
+// The lane's scale from what load_batch read: fp32 bits, or its half of the lane pair's two fp16 scales.
+template <int SF32>
+__device__ __forceinline__ float scale_of(uint32_t v) {
+    if constexpr (SF32) return __uint_as_float(v);
+    return f16_bits_to_f32((uint16_t)((__lane_id() & 1) ? v >> 16 : v));
 }
 
 // groups of one batch, added to the lane's running sum in chunk order: p_g = ((float)ival * ws) * xs
@@ -118,7 +134,7 @@ template <int WB, int GSZ, int SF32>
 __device__ __forceinline__ float use_batch(float acc, int nchunks, int c0, int kw, int gpc, int g_lane, const int8_t *sxq,
                                            const float *sxs,
                                            const uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
-                                           const uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+                                           const typename Fmt<WB, GSZ, SF32>::ST (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
     using F = Fmt<WB, GSZ, SF32>;
 #pragma unroll
     for (int u = 0; u < F::UNROLL; u++) {
@@ -126,7 +142,7 @@ __device__ __forceinline__ float use_batch(float acc, int nchunks, int c0, int k
         if (c < nchunks) {
             const int g = c * gpc + g_lane;
             const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
-            const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
+            const float sc = scale_of<SF32>(sr[u]);
             float p = (float)iv * sc; // qwen.c:452, runq.c:452
             p = p * sxs[g];
             acc = acc + p;
@@ -171,14 +187,14 @@ template <int WB, int GSZ, int SF32>
 __device__ __forceinline__ void store_batch(float *sprod, int ng, int row_l, int nchunks, int c0, int kw, int gpc,
                                             int g_lane, const int8_t *sxq, const float *sxs,
                                             const uint4 (&wv)[Fmt<WB, GSZ, SF32>::UNROLL][Fmt<WB, GSZ, SF32>::PIECES],
-                                            const uint32_t (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
+                                            const typename Fmt<WB, GSZ, SF32>::ST (&sr)[Fmt<WB, GSZ, SF32>::UNROLL]) {
     using F = Fmt<WB, GSZ, SF32>;
 #pragma unroll
     for (int u = 0; u < F::UNROLL; u++) {
         const int c = c0 + u * kw, g = c * gpc + g_lane;
         if (c < nchunks && g < ng) { // groups past n (padding of the last chunk) have no slot
             const int iv = seg_dot<WB, GSZ>(wv[u], (const uint32_t *)(sxq + g * GSZ));
-            const float sc = SF32 ? __uint_as_float(sr[u]) : f16_bits_to_f32((uint16_t)sr[u]);
+            const float sc = scale_of<SF32>(sr[u]);
             float p = (float)iv * sc; // qwen.c:452, runq.c:452
             p = p * sxs[g];
             sprod[row_l * (ng + 1) + g] = p;
@@ -223,9 +239,42 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     const bool need_pos = PRO == PRO_ATTN || EPI == EPI_QKV || EPI == EPI_ARGMAX;
     const int pos = need_pos ? a.ctrl->pos : 0;
 
-    // (1) the prologue's operands for its first pass, issued first: loads complete in issue order, so
-    // waiting for these does not also wait for the weights issued after them.  Indices past the end are
-    // clamped (the values are loaded and never used).
+    // The weight stream: the batches of all the block's iterations (it0, it0 + grid, ...) form one stream per
+    // wave, bpi batches per iteration, D register buffers in a ring; the next iteration's first batches are in
+    // flight while the current one is reduced and finished.  issue() always issues a whole batch (past the
+    // stream's end, out-of-range loads that read nothing), so the number of loads behind every batch is the
+    // same on every path.
+    const int cnt_w = a.kw_base + (my_kw < a.kw_rem);           // chunks of a row-block for this wave (>= 1)
+    const int bpi = (cnt_w + F::UNROLL - 1) / F::UNROLL;         // batches per iteration
+    const int n_my = a.it_base + (it0 < a.it_rem);               // iterations it0, it0 + grid, ... < n_it
+    const int total = n_my * bpi;
+    float pre_x = 0.0f; // EPI_RESID: out[R] of the first iteration's row
+    int iss_it = it0, iss_bi = 0, iss_n = 0; // the next batch to issue, batches issued
+    const __amdgpu_buffer_rsrc_t wrs = weight_rsrc(W);
+    const uint32_t rec = (uint32_t)W.rec, rb_bytes = (uint32_t)W.nchunks * rec;
+    auto issue = [&](uint4 (&w)[F::UNROLL][F::PIECES], typename F::ST (&sr)[F::UNROLL]) {
+        const int b = min(iss_it * a.nb + my_nb, W.nblocks - 1);
+        load_batch<WB, GSZ, SF32, NT ? 2 : 0>(wrs, (uint32_t)b * rb_bytes, rec, W.nchunks, my_kw + iss_bi * F::UNROLL * a.kw, a.kw,
+                                  lane, iss_n < total, w, sr);
+        iss_n++;
+        if (++iss_bi == bpi) {
+            iss_bi = 0;
+            iss_it += gridDim.x;
+        }
+    };
+    uint4 wr[D][F::UNROLL][F::PIECES];
+    typename F::ST sr[D][F::UNROLL];
+    // The attention merge needs the position before it can read its operands: one weight batch goes out
+    // first and is in flight meanwhile.
+    constexpr int D_PRE = PRO == PRO_ATTN ? 1 : 0;
+#pragma unroll
+    for (int d = 0; d < D_PRE; d++) issue(wr[d], sr[d]);
+
+    // (1) the prologue's operands for its first pass, issued before the rest of the weights: loads complete
+    // in issue order, so waiting for these does not also wait for the weights issued after them.  Indices
+    // past the end are clamped (the values are loaded and never used).  Vectors beyond the first pass (longer
+    // inputs than the block covers) are loaded and parked in LDS here too, so that no load issued after the
+    // weights has to be waited for before the weights are used.
     u32x4 px[PRO_VEC];      // PRO_XQ: 16 int8 activations each
     float pxs[2];           // PRO_XQ: group scales
     float4 pn[PRO_VEC], pg[PRO_VEC]; // PRO_NORM: x and gains
@@ -239,6 +288,8 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         for (int k = 0; k < PRO_VEC; k++) px[k] = src[min(tid + k * nt, nq - 1)];
 #pragma unroll
         for (int k = 0; k < 2; k++) pxs[k] = a.xs[min(tid + k * nt, W.ng - 1)];
+        for (int i = PRO_VEC * nt + tid; i < nq; i += nt) ((u32x4 *)sxq)[i] = src[i];
+        for (int i = 2 * nt + tid; i < W.ng; i += nt) sxs[i] = a.xs[i];
     } else if constexpr (PRO == PRO_NORM) {
         const float4 *x4 = (const float4 *)a.x, *w4 = (const float4 *)a.norm_w;
         const int nv = n / 4;
@@ -247,6 +298,11 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
             const int i = min(tid + k * nt, nv - 1);
             pn[k] = x4[i];
             pg[k] = w4[i];
+        }
+        float4 *sv4 = (float4 *)sv; // x in sv, gains in the n floats after it
+        for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
+            sv4[i] = x4[i];
+            sv4[nv + i] = w4[i];
         }
     } else if constexpr (PRO == PRO_ATTN) {
         const int hs = a.head_size, SP = a.att_splits, nh = a.n_heads;
@@ -263,33 +319,9 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
 
     asm volatile("" ::: "memory"); // keep the issue order: prologue operands, then weights
 
-    // (2) the wave's first D weight batches.  The batches of all the block's iterations (it0, it0 + grid,
-    // ...) form one stream per wave: bpi batches per iteration, D register buffers in a ring, and the next
-    // iteration's first batches are in flight while the current one is reduced and finished.
-    const int cnt_w = a.kw_base + (my_kw < a.kw_rem);           // chunks of a row-block for this wave (>= 1)
-    const int bpi = (cnt_w + F::UNROLL - 1) / F::UNROLL;         // batches per iteration
-    const int n_my = a.it_base + (it0 < a.it_rem);               // iterations it0, it0 + grid, ... < n_it
-    const int total = n_my * bpi;
-    float pre_x = 0.0f, pre_x_next = 0.0f; // EPI_RESID: out[R] of this / the next iteration's row
-    int iss_it = it0, iss_bi = 0;          // the next batch to issue
-    const __amdgpu_buffer_rsrc_t wrs = weight_rsrc(W);
-    const uint32_t rec = (uint32_t)W.rec, rb_bytes = (uint32_t)W.nchunks * rec;
-    auto issue = [&](uint4 (&w)[F::UNROLL][F::PIECES], uint32_t (&sr)[F::UNROLL]) {
-        const int b = min(iss_it * a.nb + my_nb, W.nblocks - 1);
-        load_batch<WB, GSZ, SF32, NT ? 2 : 0>(wrs, (uint32_t)b * rb_bytes, rec, W.nchunks, my_kw + iss_bi * F::UNROLL * a.kw, a.kw,
-                                  lane, w, sr);
-        if constexpr (EPI == EPI_RESID)
-            if (iss_bi == 0 && iss_it != it0) pre_x_next = a.out[min(iss_it * rows_it + tid, W.rows - 1)];
-        if (++iss_bi == bpi) {
-            iss_bi = 0;
-            iss_it += gridDim.x;
-        }
-    };
-    uint4 wr[D][F::UNROLL][F::PIECES];
-    uint32_t sr[D][F::UNROLL];
+    // (2) the wave's first D weight batches
 #pragma unroll
-    for (int d = 0; d < D; d++)
-        if (total > d) issue(wr[d], sr[d]);
+    for (int d = D_PRE; d < D; d++) issue(wr[d], sr[d]);
 
     // (3) the epilogue operands of this thread's first row (clamped row index, used only for valid rows)
     float pre_b = 0.0f, pre_bp = 0.0f, pre_c = 0.0f, pre_s = 0.0f;
@@ -297,22 +329,29 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         const int R = min(it0 * rows_it + tid, W.rows - 1);
         if constexpr (EPI == EPI_RESID) pre_x = a.out[R];
         if constexpr (EPI == EPI_QKV) {
+            // the same loads on both pairings (the interleaved pairing has no bias: out-of-range reads)
             const int half = a.head_size / 2, rot = a.dim + a.kv_dim, Rr = min(R, rot - 1);
-            int i;
-            if (a.rope_kind == ROPE_NEOX) {
+            const bool neox = a.rope_kind == ROPE_NEOX;
+            int i, ib = 0, ibp = 0;
+            if (neox) {
                 int e, ep;
                 bool first;
                 qkv_neox_row(Rr, a.head_size, &e, &ep, &i, &first);
-                pre_b = a.bias[R < rot ? e : R];
-                pre_bp = a.bias[R < rot ? ep : R];
+                ib = R < rot ? e : R;
+                ibp = R < rot ? ep : R;
             } else {
                 const int e = Rr < a.dim ? Rr : Rr - a.dim;
                 i = (e % a.head_size) / 2;
             }
+            const __amdgpu_buffer_rsrc_t brs =
+                __builtin_amdgcn_make_buffer_rsrc((void *)a.bias, 0, a.bias ? W.rows * 4 : 0, 0x00020000);
+            pre_b = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs, neox ? ib * 4 : (int)OOB_OFFSET, 0, 0));
+            pre_bp = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(brs, neox ? ibp * 4 : (int)OOB_OFFSET, 0, 0));
             pre_c = a.rope_cos[(size_t)pos * half + i];
             pre_s = a.rope_sin[(size_t)pos * half + i];
         }
     }
+    asm volatile("" ::: "memory"); // every load above is issued before the prologue's work begins
 
     KERNEL_MARK(1);
     // (4) prologue: int8 activations and their scales into LDS
@@ -324,10 +363,8 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         // (an unconditional use keeps the compiler from moving the loads down to here)
 #pragma unroll
         for (int k = 0; k < PRO_VEC; k++) dst[min(tid + k * nt, nq - 1)] = px[k];
-        for (int i = PRO_VEC * nt + tid; i < nq; i += nt) dst[i] = ((const u32x4 *)a.xq)[i];
 #pragma unroll
         for (int k = 0; k < 2; k++) sxs[min(tid + k * nt, W.ng - 1)] = pxs[k];
-        for (int i = 2 * nt + tid; i < W.ng; i += nt) sxs[i] = a.xs[i];
     } else {
         float4 *sv4 = (float4 *)sv;
         if constexpr (PRO == PRO_NORM) {
@@ -343,11 +380,9 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                     part += v.z * v.z;
                     part += v.w * v.w;
                 }
-            // vectors beyond the first pass are parked in LDS (x in sv, gains in the n floats after it)
+            // vectors beyond the first pass were parked in LDS by this same thread (x in sv, gains after it)
             for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
-                const float4 v = ((const float4 *)a.x)[i], g = ((const float4 *)a.norm_w)[i];
-                sv4[i] = v;
-                sv4[nv + i] = g;
+                const float4 v = sv4[i];
                 part += v.x * v.x;
                 part += v.y * v.y;
                 part += v.z * v.z;
@@ -468,8 +503,9 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         if constexpr (EPI == EPI_STORE) {
             if (tid < rows_it && R < W.rows) a.out[R] = srow[tid];
         } else if constexpr (EPI == EPI_RESID) {
-            if (tid < rows_it && R < W.rows) a.out[R] = pre_x + srow[tid]; // qwen.c:551, 565
-            pre_x = pre_x_next;
+            // the first iteration's operand was read at the start; later ones (blocks of several
+            // iterations) read theirs here
+            if (tid < rows_it && R < W.rows) a.out[R] = (first_it ? pre_x : a.out[R]) + srow[tid]; // qwen.c:551, 565
         } else if constexpr (EPI == EPI_ARGMAX) {
             if (tid < rows_it && R < W.rows) {
                 const float v = srow[tid];
@@ -550,7 +586,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     // (6) the stream: consume a batch, refill its buffer with the batch D ahead
     int use_it = it0, use_bi = 0;
     float acc = 0.0f;
-    auto consume = [&](const uint4 (&w)[F::UNROLL][F::PIECES], const uint32_t (&sr)[F::UNROLL]) {
+    auto use = [&](const uint4 (&w)[F::UNROLL][F::PIECES], const typename F::ST (&sr)[F::UNROLL]) {
         if (use_it * a.nb + my_nb < W.nblocks) {
             if (a.ord)
                 store_batch<WB, GSZ, SF32>(sprod, W.ng, my_nb * rb + (lane & (rb - 1)), W.nchunks,
@@ -559,20 +595,43 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                 acc = use_batch<WB, GSZ, SF32>(acc, W.nchunks, my_kw + use_bi * F::UNROLL * a.kw, a.kw, gpc, g_lane,
                                               sxq, sxs, w, sr);
         }
-        if (++use_bi == bpi) {
-            finish(use_it, acc);
-            acc = 0.0f;
-            use_bi = 0;
-            use_it += gridDim.x;
-        }
+        use_bi++;
     };
-    for (int q = 0; q < total; q += D) {
+    if constexpr (EPI == EPI_ARGMAX) {
+        // several iterations per block (a persistent grid over the long head): reduce and finish each
+        // iteration as its last batch is used, while the next iteration's batches are in flight
+        for (int q = 0; q < total; q += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                if (q + d < total) {
+                    use(wr[d], sr[d]);
+                    if (use_bi == bpi) {
+                        finish(use_it, acc);
+                        acc = 0.0f;
+                        use_bi = 0;
+                        use_it += gridDim.x;
+                    }
+                }
+                issue(wr[d], sr[d]); // past the stream's end: loads that read nothing
+            }
+        }
+    } else {
+        // one iteration per block (the launcher runs one block per iteration).  Whole rounds of D uses, each
+        // refilling its buffer, while a later round remains; then the last round uses what is in flight.
+        // Batches past this wave's count (at most D - 1, when D does not divide it) read nothing.
+        const int nbat_r = (total + D - 1) / D * D;
+        int j = 0;
+        for (; j < nbat_r - D; j += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                use(wr[d], sr[d]);
+                issue(wr[d], sr[d]);
+            }
+        }
 #pragma unroll
         for (int d = 0; d < D; d++)
-            if (q + d < total) {
-                consume(wr[d], sr[d]);
-                if (q + d + D < total) issue(wr[d], sr[d]);
-            }
+            if (j + d < total) use(wr[d], sr[d]);
+        finish(it0, acc);
     }
     if constexpr (EPI == EPI_ARGMAX) {
         // block argmax: larger value wins, equal values keep the lower row (first strict maximum)
@@ -612,9 +671,9 @@ template <int WB, int GSZ, int SF32, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
     const int threads = a.kw * a.nb * WAVE;
     const size_t lds = gemv_lds_bytes(a, PRO, EPI, threads);
-    if (a.depth == 4) {
-        if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4, 1>), dim3(grid), dim3(threads), lds, st, a);
-        else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 4, 0>), dim3(grid), dim3(threads), lds, st, a);
+    if (a.depth == 1) {
+        if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 1, 1>), dim3(grid), dim3(threads), lds, st, a);
+        else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 1, 0>), dim3(grid), dim3(threads), lds, st, a);
     } else {
         if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 1>), dim3(grid), dim3(threads), lds, st, a);
         else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 0>), dim3(grid), dim3(threads), lds, st, a);
@@ -653,11 +712,12 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
     a.kw_rem = a.W.nchunks % a.kw;
     a.it_base = a.n_it / grid;
     a.it_rem = a.n_it % grid;
-    // stream depth: 2 or 4 batches in flight per wave.  The residual epilogue preloads the next iteration's
-    // output rows one iteration ahead, which needs at least depth - 1 batches per iteration.
+    // one block per iteration, except the head's argmax epilogue (a persistent grid over the head's rows)
+    if (epi != EPI_ARGMAX && grid != a.n_it) return hipErrorInvalidValue;
+    // stream depth: 2 batches in flight per wave when some wave has a second batch to read, else 1
     const int pieces = gs * wbits / 8 / 16, unroll = pieces > 0 && pieces <= 4 ? 4 / pieces : 1; // Fmt::UNROLL
-    // Depth 4 holds twice the registers: blocks of at most 8 waves.
-    if (a.depth != 4 || a.kw * a.nb > 8 || (epi == EPI_RESID && (a.kw_base + unroll - 1) / unroll < 3)) a.depth = 2;
+    const int max_total = (a.kw_base + (a.kw_rem > 0) + unroll - 1) / unroll * (a.it_base + (a.it_rem > 0));
+    a.depth = a.depth != 1 && max_total >= 2 ? 2 : 1;
     // the prologues read their inputs as 16-byte vectors (8 bytes for the attention statistics)
     auto al = [](const void *p, uintptr_t m) { return ((uintptr_t)p & (m - 1)) == 0; };
     if (a.W.n % 32 || a.W.bytes >= 0x7fffffffu || (pro == PRO_XQ && !al(a.xq, 16)) || (pro == PRO_NORM && (!al(a.x, 16) || !al(a.norm_w, 16))) ||
