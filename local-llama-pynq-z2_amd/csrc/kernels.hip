@@ -215,6 +215,9 @@ typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 template <int WB, int GSZ, int SF32, int PRO, int EPI, int D, int NT>
 __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
     using F = Fmt<WB, GSZ, SF32>;
+    // the activation quantization flavour follows the weight format: fp16 scales are the Qwen .qwb path
+    // (qwen.c quantize), fp32 scales the llama2.c .bin path (runq.c quantize); the launcher checks it
+    constexpr int QF = SF32 ? QF_RUNQ : QF_QWEN;
     extern __shared__ __align__(16) uint8_t lds[];
     const TiledMat &W = a.W;
     const int rb = W.rb, gpc = WAVE / rb, ngp = W.nchunks * gpc, ngp4 = (ngp + 3) & ~3;
@@ -412,7 +415,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                         const int i = tid + k * nt;
                         const float4 v = pn[k], g = pg[k];
                         const float4 o = make_float4(g.x * (ss * v.x), g.y * (ss * v.y), g.z * (ss * v.z), g.w * (ss * v.w));
-                        quantize_slot(o, i, i < nv, W.gs, a.qflavor, sxq, sxs);
+                        quantize_slot(o, i, i < nv, GSZ, QF, sxq, sxs);
                     }
             } else {
 #pragma unroll
@@ -466,7 +469,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         if (!in_regs) {
             __syncthreads();
             KERNEL_MARK(3);
-            block_quantize(sv, n, W.gs, a.qflavor, sxq, sxs);
+            block_quantize(sv, n, GSZ, QF, sxq, sxs);
         }
         for (int i = n + tid; i < ngp * GSZ; i += nt) sxq[i] = 0;
     }
@@ -577,7 +580,7 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
                 const int cnt = min(per_it, a.dim - j0);
                 if (a.hf)
                     for (int i = tid; i < cnt; i += nt) a.hf[j0 + i] = sv[i];
-                block_quantize(sv, cnt, W.gs, a.qflavor, a.hq + j0, a.hs + j0 / W.gs);
+                block_quantize(sv, cnt, GSZ, QF, a.hq + j0, a.hs + j0 / GSZ);
             }
         }
         __syncthreads();
@@ -712,6 +715,9 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
     a.kw_rem = a.W.nchunks % a.kw;
     a.it_base = a.n_it / grid;
     a.it_rem = a.n_it % grid;
+    // the kernels quantize activations in the flavour of their weight format (QF in k_gemv)
+    if (pro != PRO_XQ || epi == EPI_SWIGLU)
+        if (a.qflavor != (sf32 ? QF_RUNQ : QF_QWEN) || a.W.gs != gs) return hipErrorInvalidValue;
     // one block per iteration, except the head's argmax epilogue (a persistent grid over the head's rows)
     if (epi != EPI_ARGMAX && grid != a.n_it) return hipErrorInvalidValue;
     // stream depth: 2 batches in flight per wave when some wave has a second batch to read, else 1
