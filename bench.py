@@ -7,6 +7,7 @@ greedy, batch 1.  A step is one decode position: the whole forward() plus the ar
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
   python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu] [--no-counters]
+                  [--no-c5] [--no-strict]
   The default run (c3) also measures the Qwen2-7B shape (c5) and reports it as the sub-record "c5".
   roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes that the
   run starts itself as child processes (FETCH_SIZE, then WRITE_SIZE, over `bench.py --counters`: a calibration
@@ -384,14 +385,16 @@ def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters):
                   for s in stats}
 
     # the strict (reference-order) mode: the same greedy workload, and its decode rate
-    if not a.strict:
-        m.set_strict(True)
-    gs = m.generate(prompt, cpu_tokens, logits=True)
-    ids_strict, lg_strict = [int(v) for v in gs["ids"]], gs["logits"]
-    m.generate(prompt, 1)
-    sst = min(steps, 32)
-    strict_tok_s = sst / (m.decode_replay(sst) * 1e-3)
-    log(f"[{name}] strict mode: {strict_tok_s:.1f} tok/s")
+    ids_strict = lg_strict = strict_tok_s = None
+    if not a.no_strict:
+        if not a.strict:
+            m.set_strict(True)
+        gs = m.generate(prompt, cpu_tokens, logits=True)
+        ids_strict, lg_strict = [int(v) for v in gs["ids"]], gs["logits"]
+        m.generate(prompt, 1)
+        sst = min(steps, 32)
+        strict_tok_s = sst / (m.decode_replay(sst) * 1e-3)
+        log(f"[{name}] strict mode: {strict_tok_s:.1f} tok/s")
     n_logits = m.info.n_logits
     m.close()
 
@@ -425,7 +428,7 @@ def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters):
         "kernels_in_graph": per_kernel,
         "cpu_baseline": cpu,
         "greedy_vs_reference": (fast_parity(ref, prompt, ids_fast, lg_fast) if not a.strict else None) if ref else None,
-        "strict_vs_reference": strict_parity(ref, ids_strict, lg_strict, strict_tok_s) if ref else None,
+        "strict_vs_reference": strict_parity(ref, ids_strict, lg_strict, strict_tok_s) if ref and ids_strict else None,
     }
 
 
@@ -441,6 +444,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="no reference runs (parity lines, CPU baseline)")
     ap.add_argument("--no-counters", action="store_true", help="no rocprofv3 counter passes (roofline.traffic null)")
     ap.add_argument("--no-c5", action="store_true", help="no Qwen2-7B-shape sub-record in the default run")
+    ap.add_argument("--no-strict", action="store_true",
+                    help="no strict-mode run after the fast mode (profiles of the fast mode's kernels alone)")
     ap.add_argument("--strict", action="store_true",
                     help="time the strict (reference-order, bitwise) mode instead of the fast mode")
     ap.add_argument("--sample", default=None, metavar="T,P,SEED",

@@ -7,11 +7,11 @@
 // split over kw waves, and an iteration is nb row-blocks.  Epilogues that need whole groups of rows fix nb:
 // SwiGLU quantizes gs hidden values per group, each row-block yields rb/2 of them.
 //   Latency shape (when every iteration's block fits on the chip at once, 16 waves per CU): about 4 chunks
-//   per wave and one iteration per block, so all loads are in flight together and a block's latency chain
-//   is one round trip plus its prologue.
-//   Streaming shape (larger matrices): about 16 chunks per wave, blocks of at least 4 waves, and a
-//   persistent grid of as many blocks as fit at once; each block pays its prologue once and streams its
-//   iterations back to back.
+//   per wave, so all loads are in flight together and a block's latency chain is one round trip plus its
+//   prologue.
+//   Streaming shape (larger matrices): about 16 chunks per wave (a whole row-block per wave for SwiGLU).
+//   Every GEMV runs one block per iteration, except the head's argmax and ordered sums: a persistent grid of
+//   as many blocks as fit at once, each paying its prologue once and streaming its iterations back to back.
 static void gemv_split(GemvShape &s, int C, int per_wave, const TiledMat &T, int epi) {
     s.kw = (C + per_wave - 1) / per_wave;
     if (s.kw > 16) s.kw = 16;
@@ -50,15 +50,15 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     if (iters > resident) {
         if (!ordered) {
             // streaming split: about 16 chunks per wave; the SwiGLU epilogue's blocks (4 row-blocks, 32 hidden
-            // values) measured fastest with one wave per row-block reading all of its chunks
-            gemv_split(s, C, epi == EPI_SWIGLU ? C : 16, T, epi);
+            // values) measured fastest with one wave per row-block reading all of its chunks (unordered sums)
+            gemv_split(s, C, epi == EPI_SWIGLU && !s.ord ? C : 16, T, epi);
             if (s.ord && (size_t)s.nb * T.rb * (T.ng + 1) * 4 > 65536) s.nb = 1; // keep the products in LDS
             iters = (T.nblocks + s.nb - 1) / s.nb;
             waves = s.kw * s.nb;
             resident = cus * (waves < 16 ? 16 / waves : 1);
         }
-        // the head's argmax runs a persistent grid; every other GEMV one block per iteration
-        s.grid = epi == EPI_ARGMAX && iters > resident ? resident : iters;
+        // the head's argmax and ordered sums run a persistent grid; every other GEMV one block per iteration
+        s.grid = (epi == EPI_ARGMAX || s.ord) && iters > resident ? resident : iters;
     } else {
         // latency shape: when the iterations outnumber the CUs, some CUs hold two blocks and finish last;
         // more row-blocks per iteration (more waves per block) keep it at one block per CU (a wider rule that

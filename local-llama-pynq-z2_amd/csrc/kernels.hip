@@ -600,9 +600,10 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
         }
         use_bi++;
     };
-    if constexpr (EPI == EPI_ARGMAX) {
-        // several iterations per block (a persistent grid over the long head): reduce and finish each
-        // iteration as its last batch is used, while the next iteration's batches are in flight
+    if (EPI == EPI_ARGMAX || a.ord) {
+        // several iterations per block (a persistent grid over the long head, or ordered sums, whose per-row
+        // running sums at the end of an iteration are long): reduce and finish each iteration as its last
+        // batch is used, while the next iteration's batches are in flight
         for (int q = 0; q < total; q += D) {
 #pragma unroll
             for (int d = 0; d < D; d++) {
@@ -718,8 +719,8 @@ hipError_t launch_gemv(int wbits, int gs, int sf32, int pro, int epi, const Gemv
     // the kernels quantize activations in the flavour of their weight format (QF in k_gemv)
     if (pro != PRO_XQ || epi == EPI_SWIGLU)
         if (a.qflavor != (sf32 ? QF_RUNQ : QF_QWEN) || a.W.gs != gs) return hipErrorInvalidValue;
-    // one block per iteration, except the head's argmax epilogue (a persistent grid over the head's rows)
-    if (epi != EPI_ARGMAX && grid != a.n_it) return hipErrorInvalidValue;
+    // one block per iteration, except the head's argmax epilogue and ordered sums (persistent grids)
+    if (epi != EPI_ARGMAX && !a.ord && grid != a.n_it) return hipErrorInvalidValue;
     // stream depth: 2 batches in flight per wave when some wave has a second batch to read, else 1
     const int pieces = gs * wbits / 8 / 16, unroll = pieces > 0 && pieces <= 4 ? 4 / pieces : 1; // Fmt::UNROLL
     const int max_total = (a.kw_base + (a.kw_rem > 0) + unroll - 1) / unroll * (a.it_base + (a.it_rem > 0));
