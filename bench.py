@@ -8,6 +8,8 @@ hipGraph replay.  `value` = timed steps / wall time between two device-wide sync
 
   python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu] [--no-counters]
                   [--no-c5] [--no-strict]
+  python bench.py --traffic-from D --traffic-all     (every kernel kind's HBM bytes per launch from the passes in D)
+  python bench.py --trace-summary T.csv              (a rocprofv3 kernel trace grouped by kernel and grid)
   The default run (c3) also measures the Qwen2-7B shape (c5) and reports it as the sub-record "c5".
   roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes that the
   run starts itself as child processes (FETCH_SIZE, then WRITE_SIZE, over `bench.py --counters`: a calibration
@@ -241,6 +243,21 @@ def traffic_from(pmc_dir, kind):
     return res
 
 
+def trace_summary(csv_path):
+    """a rocprofv3 --kernel-trace CSV grouped by (kernel, grid, workgroup): share of GPU time, calls, avg / median /
+    min / max microseconds (the prefill GEMM shapes share one kernel name and differ by grid)"""
+    import csv
+    groups = {}
+    for r in csv.DictReader(open(csv_path)):
+        key = (r["Kernel_Name"], r.get("Grid_Size", ""), r.get("Workgroup_Size", ""))
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    total = sum(sum(v) for v in groups.values())
+    for (name, grid, wg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        v.sort()
+        print(f"{sum(v) / total * 100:6.2f}%  calls {len(v):6d}  avg {sum(v) / len(v):9.2f}  med {v[len(v) // 2]:9.2f}  "
+              f"min {v[0]:9.2f}  max {v[-1]:9.2f}  grid {grid:>9} wg {wg:>5}  {name}")
+
+
 def layer_macs(info):
     """multiply-accumulates of the layer matrices for one token (qkv, o, gate/up, down)"""
     kv = info.dim // info.n_heads * info.n_kv_heads
@@ -455,7 +472,20 @@ def main():
                     help="counter pass: the calibration copy, then the prompt and --profile-steps decode steps as "
                          "eager launches only (no graphs), no report")
     ap.add_argument("--traffic-from", default=None, help="directory with the FETCH_SIZE/WRITE_SIZE passes")
+    ap.add_argument("--traffic-all", action="store_true",
+                    help="with --traffic-from: print every kernel kind's HBM bytes per launch and stop")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="print a rocprofv3 kernel trace grouped by kernel and grid, and stop")
     a = ap.parse_args()
+    if a.trace_summary:
+        return trace_summary(a.trace_summary)
+    if a.traffic_from and a.traffic_all:
+        for kind in KERNEL_SYMBOL:
+            r = traffic_from(a.traffic_from, kind)
+            if r:
+                print(f"{kind:14s} fetched {r['fetch'] / 1e6:9.3f} MB  written {r['write'] / 1e6:8.3f} MB per launch "
+                      f"(counter factors {r['fetch_factor']:.3f} / {r['write_factor']:.3f})")
+        return
     if a.gpus != 1:
         print(f"bench.py runs on one GPU: the decode path has no multi-GPU form (asked for --gpus {a.gpus})",
               file=sys.stderr)
