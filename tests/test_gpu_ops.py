@@ -9,7 +9,7 @@ import os
 import numpy as np
 import pytest
 
-from helpers import GOLDEN, exact_terms, f16_scales, oracle, pkg, ptr, unpack_q4
+from helpers import GOLDEN, exact_terms, f16_scales, oracle, pkg, ptr, synth, unpack_q4
 
 pytestmark = pytest.mark.gpu
 OPS = np.load(os.path.join(GOLDEN, "ops.npz"))
@@ -116,6 +116,70 @@ def test_matvec4_special_fp16_scales(drv, bits):
     wv = unpack_q4(w, d, n) if bits == 4 else w.view(np.int8).reshape(d, n)
     ref, mag, _ = exact_terms(wv, s.view(np.float16).astype(np.float32), xq, xs)
     assert (np.abs(out - ref) <= 1e-5 * mag).all()
+
+
+def qwb_matrix(path, kind, layer):
+    """matrix `kind` (0..6: wq, wk, wv, wo, w1 gate, w2 down, w3 up) of `layer`, or the head (kind 7), read from
+    a .qwb the way the reference testbench walks it (hls4/matvec4_tb.cpp:102-126): every array padded to 64
+    bytes; the per-layer vectors (two norms, the q/k/v biases), the output norm and the head ids, then the
+    matrices as weight plane + fp16 scale plane.  Returns (weights, scales, n, d, bits)."""
+    with open(path, "rb") as f:
+        f.seek(8)
+        dim, hid, L, nh, nkv, vocab, head_k, ctx, gs, emb_bits = np.frombuffer(f.read(40), "<i4")
+        kv = dim // nh * nkv
+        off = 256
+
+        def take(nbytes):
+            nonlocal off
+            at = off
+            off += nbytes + (-(off + nbytes) & 63)
+            return at
+        for n in (dim, dim, dim, kv, kv):
+            for _ in range(L):
+                take(4 * n)
+        take(4 * dim)
+        take(4 * head_k)
+        shapes = [(dim, dim), (kv, dim), (kv, dim), (dim, dim), (hid, dim), (dim, hid), (hid, dim)]
+        for i in range(7 * L + 1):
+            rows, n = shapes[i // L] if i < 7 * L else (head_k, dim)
+            bits = 4 if i < 7 * L else int(emb_bits)
+            wo, so = take(rows * n * bits // 8), take(rows * n // 32 * 2)
+            if i == kind * L + layer:
+                f.seek(wo)
+                w = np.frombuffer(f.read(rows * n * bits // 8), np.uint8)
+                f.seek(so)
+                s = np.frombuffer(f.read(rows * n // 32 * 2), np.uint16)
+                return w, s, int(n), int(rows), bits
+    raise ValueError("no such matrix")
+
+
+@pytest.fixture(scope="module")
+def c3_qwb(tmp_path_factory):
+    # the reference testbench's real-matrix file is the 24-layer Qwen2.5-0.5B .qwb with a 49152-row head; the
+    # same shapes and layout, seeded synthetic Q4_0 / Q8_0 data (no model files here)
+    p = str(tmp_path_factory.mktemp("realmat") / "c3h49k.qwb")
+    return synth("qwb", p, "c3", 17, "vocab=65536", "head_k=49152")
+
+
+@pytest.mark.parametrize("name,kind,layer", [("blk.0 attn_q", 0, 0), ("blk.0 attn_k", 1, 0),
+                                             ("blk.23 ffn_gate", 4, 23), ("blk.0 ffn_down", 5, 0),
+                                             ("blk.12 ffn_up", 6, 12), ("output head", 7, 0)])
+def test_matvec4_testbench_real_matrices(drv, c3_qwb, name, kind, layer):
+    """the testbench's real-matrix mode (hls4/matvec4_tb.cpp:150-164): the matrices it names, read from the
+    file, through the drop-in with its activation distributions (xq uniform in [-128, 127], xs in [1e-3, 1e-1])
+    and its bar, |out - ref| <= 1e-5 * sum_g |term_g| per row, and against the oracle's sequential sum"""
+    w, s, n, d, bits = qwb_matrix(c3_qwb, kind, layer)
+    rng = np.random.default_rng(4321 + kind * 100 + layer)
+    xq = rng.integers(-128, 128, size=n, dtype=np.int8)
+    xs = rng.uniform(1e-3, 1e-1, size=n // 32).astype(np.float32)
+    out = run_matvec4(drv, w, s, xq, xs, n, d, bits)
+    wv = unpack_q4(w, d, n) if bits == 4 else w.view(np.int8).reshape(d, n)
+    ref, mag, _ = exact_terms(wv, s.view(np.float16).astype(np.float32), xq, xs)
+    err = np.abs(out.astype(np.float64) - ref)
+    assert (err <= 1e-5 * mag).all(), (name, float((err / np.maximum(mag, 1e-30)).max()))
+    o = np.empty(d, np.float32)
+    oracle().or_matvec4(ptr(o), ptr(w), ptr(s), ptr(xq), ptr(xs), n, d, bits)
+    assert (np.abs(out.astype(np.float64) - o) <= 2e-5 * mag).all(), name
 
 
 @pytest.mark.parametrize("k", range(5))
