@@ -249,7 +249,10 @@ def trace_summary(csv_path):
     import csv
     groups = {}
     for r in csv.DictReader(open(csv_path)):
-        key = (r["Kernel_Name"], r.get("Grid_Size", ""), r.get("Workgroup_Size", ""))
+        # rocprofv3 writes Grid_Size / Workgroup_Size, or per-axis columns (Grid_Size_X, ...), by version
+        grid = r.get("Grid_Size") or "x".join(r.get(f"Grid_Size_{c}", "") for c in "XYZ").strip("x")
+        wg = r.get("Workgroup_Size") or r.get("Workgroup_Size_X", "")
+        key = (r["Kernel_Name"], grid, wg)
         groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
     total = sum(sum(v) for v in groups.values())
     for (name, grid, wg), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):

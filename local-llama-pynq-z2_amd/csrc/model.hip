@@ -96,6 +96,11 @@ struct llm_model {
     float *pf_ml = nullptr, *pf_acc = nullptr; // attention slice partials
     int8_t *pf_a = nullptr;
     int *pf_ids = nullptr;
+    // h of the SwiGLU in the gate/up GEMM's epilogue (the down GEMM's input; pf_a is the gate/up input then),
+    // on by default where the shapes allow it (LLM_PF_SWIGLU=0 at llm_open: the separate SwiGLU kernel)
+    int8_t *pf_h = nullptr;
+    float *pf_hs = nullptr;
+    int pf_swiglu = 1;
     // file mapping during load
     const uint8_t *file = nullptr;
     size_t file_size = 0;
@@ -522,6 +527,7 @@ int finish_setup(llm_model *m) {
     m->head_nt = m->weights_nt;
     if (const char *e = getenv("LLM_WEIGHTS_NT")) m->weights_nt = m->head_nt = atoi(e) != 0; // 0 / 1: override
     if (const char *e = getenv("LLM_HEAD_NT")) m->head_nt = atoi(e) != 0;
+    if (const char *e = getenv("LLM_PF_SWIGLU")) m->pf_swiglu = atoi(e) != 0;
     return 0;
 }
 
@@ -823,7 +829,8 @@ int prefill_alloc(llm_model *m, int M) {
     const llm_info &I = m->info;
     const int dim = I.dim, hid = I.hidden_dim, rows = std::max(dim + 2 * m->kv_dim, 2 * hid), wmax = std::max(dim, hid);
     for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_s,
-                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
+                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc, (void *)m->pf_h,
+                    (void *)m->pf_hs})
         if (p) hipFree(p);
     m->pf_cap = 0;
     // the GEMM input in token-block tiles (rounded up to 16 tokens, whole chunk pairs and scale quads)
@@ -832,7 +839,9 @@ int prefill_alloc(llm_model *m, int M) {
         hipMalloc(&m->pf_s, pf_scale_floats(wmax / m->gs, M) * 4) != hipSuccess ||
         hipMalloc(&m->pf_a, pf_act_bytes(wmax, M)) != hipSuccess || hipMalloc(&m->pf_ids, (size_t)M * 4) != hipSuccess ||
         hipMalloc(&m->pf_ml, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * 2 * 4) != hipSuccess ||
-        hipMalloc(&m->pf_acc, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * m->hs * 4) != hipSuccess) {
+        hipMalloc(&m->pf_acc, (size_t)M * I.n_heads * PREFILL_ATT_SMAX * m->hs * 4) != hipSuccess ||
+        hipMalloc(&m->pf_h, pf_act_bytes(hid, M)) != hipSuccess ||
+        hipMalloc(&m->pf_hs, pf_scale_floats(hid / m->gs, M) * 4) != hipSuccess) {
         fprintf(stderr, "llm_prefill: cannot allocate the activations of %d tokens\n", M);
         return -1;
     }
@@ -884,6 +893,15 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     g.y = m->pf_y;
     g.M = M;
     g.simds = 4 * hip_cu_count(m->device);
+    g.qflavor = m->qflavor;
+    g.strict = m->strict;
+    g.hq = m->pf_h;
+    g.hsc = m->pf_hs;
+    // the SwiGLU epilogue takes int4 gate/up rows in blocks of 8 + 8, groups of 32 and the 16 x 16 .. 32 x 32
+    // tiles (the shape the gate/up GEMM gets for M tokens)
+    const int gu_shape = pgemm_pick_shape(m->L[0].gu.rows, M, g.simds);
+    const bool fuse_swiglu = m->pf_swiglu && wb == 4 && m->gs == 32 && m->L[0].gu.rb == 16 &&
+                             m->L[0].gu.rows % 64 == 0 && (gu_shape == 11 || gu_shape == 22);
     for (int l = 0; l < I.n_layers; l++) {
         const Layer &Ly = m->L[l];
         pa.kc = m->kc + (size_t)l * m->ctx * kv;
@@ -901,11 +919,21 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
         pa.norm_w = ffn_norm(m, l);
         HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, true, m->st)); // x += o output, then the FFN norm
         g.W = Ly.gu;
-        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
-        pa.gu_rb = Ly.gu.rb;
-        HIP_OR_FAIL("llm_prefill", launch_p_swiglu_quant(pa, m->st));
+        if (fuse_swiglu) { // h straight from the gate/up GEMM into pf_h, the down GEMM's input
+            g.swiglu = 1;
+            HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+            g.swiglu = 0;
+            g.xq = m->pf_h;
+            g.xs = m->pf_hs;
+        } else {
+            HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+            pa.gu_rb = Ly.gu.rb;
+            HIP_OR_FAIL("llm_prefill", launch_p_swiglu_quant(pa, m->st));
+        }
         g.W = Ly.down;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+        g.xq = m->pf_a;
+        g.xs = m->pf_s;
         if (l == I.n_layers - 1) HIP_OR_FAIL("llm_prefill", launch_p_resid(pa, m->st));
     }
     return 0;
@@ -938,7 +966,8 @@ void free_model(llm_model *m) {
     for (void *p : m->allocs) hipFree(p);
     if (m->hist) hipFree(m->hist);
     for (void *p : {(void *)m->pf_x, (void *)m->pf_y, (void *)m->pf_q, (void *)m->pf_s,
-                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc})
+                    (void *)m->pf_a, (void *)m->pf_ids, (void *)m->pf_ml, (void *)m->pf_acc, (void *)m->pf_h,
+                    (void *)m->pf_hs})
         if (p) hipFree(p);
     if (m->st) hipStreamDestroy(m->st);
     if (m->file) munmap((void *)m->file, m->file_size);

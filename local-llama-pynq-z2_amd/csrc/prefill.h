@@ -40,6 +40,12 @@ struct PgemmArgs {
     int shape;              // 0: pgemm_pick_shape; 10 TA + TB: one wave per 16 TA rows x 16 TB tokens
                             // (TA 1, 2, 4; TB 1, 2, 4; not 44)
     int simds;              // SIMDs of the device (0: 1024)
+    // swiglu = 1: W is the gate/up matrix (row-blocks of 16: 8 gate rows, then the 8 matching up rows) and the
+    // epilogue writes h = silu(gate) * up quantized (groups of 32, flavour qflavor; strict: the reference
+    // libm's expf) into the token-block tiles hq / hsc instead of y (int4 weights, shapes 11, 12, 21, 22)
+    int swiglu, qflavor, strict;
+    int8_t *hq;             // pf_act_bytes(rows / 2, M); must not alias xq
+    float *hsc;             // pf_scale_floats(rows / 64, M)
 };
 
 // Tile shape of the prefill GEMM for d output rows and M tokens on a device of `simds` SIMDs.  The smallest

@@ -80,7 +80,7 @@ __device__ __forceinline__ void lane_row_transpose(uint32_t (&x)[4]) {
     x[3] = s23[1];
 }
 
-template <int WB, int GSZ, int SF32, int TA, int TB>
+template <int WB, int GSZ, int SF32, int TA, int TB, int SWG>
 __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
     constexpr int KC = GSZ / 32;             // 32-element chunks per group
     constexpr int AP = WB == 4 ? 1 : 2 * KC; // 16-byte pieces per (row, group) weight segment
@@ -94,8 +94,25 @@ __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
     const int xt = (W.rows + 16 * TA - 1) / (16 * TA), yt = (a.M + 16 * TB - 1) / (16 * TB), y4 = (yt + 3) / 4;
     const int b = blockIdx.x, xcd = b & 7, idx = b >> 3;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tx = xcd + 8 * (idx / y4), ty = 4 * (idx - (idx / y4) * y4) + w;
-    if (tx >= xt || ty >= yt) return; // the whole wave (the waves of a block share nothing but the block)
+    // SwiGLU epilogue: a quantization group of 32 hidden values is RT row tiles (8 TA hidden values each), so a
+    // block is RT row tiles x NTY token tiles, and its waves exchange per-token maxima once at the end
+    constexpr int RT = SWG ? 4 / TA : 1, NTY = 4 / RT;
+    int tx, ty;
+    if constexpr (SWG) {
+        const int yb = (yt + NTY - 1) / NTY, gx = xcd + 8 * (idx / yb), tyb = idx - (idx / yb) * yb;
+        tx = gx * RT + w % RT;
+        ty = tyb * NTY + w / RT;
+    } else {
+        tx = xcd + 8 * (idx / y4);
+        ty = 4 * (idx - (idx / y4) * y4) + w;
+    }
+    const bool valid = tx < xt && ty < yt;
+    if constexpr (!SWG) {
+        if (!valid) return; // the whole wave (the waves of a block share nothing but the block)
+    } else { // past the matrix or the tokens: a valid tile computed again, nothing stored, for the barrier
+        tx = min(tx, xt - 1);
+        ty = min(ty, yt - 1);
+    }
     const int l = threadIdx.x & 63, q = l >> 4, c16 = l & 15;
     const int r0 = tx * 16 * TA, m0 = ty * 16 * TB, MB = (a.M + 15) >> 4;
     const int rb = W.rb, ng = W.ng, gpc = WAVE / rb, lg = 31 - __builtin_clz(gpc);
@@ -353,16 +370,74 @@ __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
             for (int ee = 0; ee < 4; ee++)
                 if (kk == k && ee == e) products(d[ee & 1], kk, ee, nullptr);
     }
+    if constexpr (!SWG) {
 #pragma unroll
-    for (int j = 0; j < TB; j++) {
-        const int m = m0 + 16 * j + c16;
-        if (m >= a.M) continue;
+        for (int j = 0; j < TB; j++) {
+            const int m = m0 + 16 * j + c16;
+            if (m >= a.M) continue;
 #pragma unroll
-        for (int i = 0; i < TA; i++) {
-            const int R = r0 + 16 * i + 4 * q; // rows % 4 == 0: R < rows means all four rows are
-            if (R < W.rows)
-                *(float4 *)(a.y + (size_t)m * W.rows + R) =
-                    make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+            for (int i = 0; i < TA; i++) {
+                const int R = r0 + 16 * i + 4 * q; // rows % 4 == 0: R < rows means all four rows are
+                if (R < W.rows)
+                    *(float4 *)(a.y + (size_t)m * W.rows + R) =
+                        make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+            }
+        }
+    } else {
+        // SwiGLU (qwen.c:556-562, runq.c:589-596) and int8 quantization of h, as k_p_swiglu_quant does it.  Row
+        // block tx TA + i holds 8 gate rows, then their 8 up rows: in the MFMA layout lane rows 0, 1 hold gate
+        // rows 4 q + r and lane rows 2, 3 the matching up rows of the same token; permlane32_swap gives every
+        // lane the other half, so each lane has (gate, up) pairs.  Lane rows 0, 1 take r = 0, 1 and lane rows
+        // 2, 3 take r = 2, 3 of gate rows 4 (q & 1) + r: h of hidden value 8 (tx TA + i) + 4 (q & 1) + r of
+        // token m0 + 16 j + c16.
+        __shared__ float s_gmax[4][16 * TB];
+        const int half = q >> 1, qq = q & 1;
+        float hv[TA][TB][2], pm[TB];
+#pragma unroll
+        for (int j = 0; j < TB; j++) pm[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TA; i++)
+#pragma unroll
+            for (int j = 0; j < TB; j++)
+#pragma unroll
+                for (int rr = 0; rr < 2; rr++) {
+                    // this lane's r = 2 half + rr: its own value, and its partner's for the same r, which the
+                    // partner sends (each lane sends the r its partner takes: rr for lane rows 0, 1, 2 + rr for 2, 3)
+                    const float own = half ? acc[i][j][2 + rr] : acc[i][j][rr];
+                    const uint32_t sb = __float_as_uint(half ? acc[i][j][rr] : acc[i][j][2 + rr]);
+                    const auto sw = __builtin_amdgcn_permlane32_swap(sb, sb, false, false);
+                    const float other = __uint_as_float(half ? sw[0] : sw[1]);
+                    const float g = half ? other : own, u = half ? own : other;
+                    const float sig = 1.0f / (1.0f + (a.strict ? ref_expf(-g) : expf(-g)));
+                    const float gs = g * sig;
+                    hv[i][j][rr] = gs * u;
+                    pm[j] = fmaxf(pm[j], fabsf(hv[i][j][rr]));
+                }
+        // the token's max over this wave's 8 TA hidden values (all four lane rows), then over the group's RT waves
+#pragma unroll
+        for (int j = 0; j < TB; j++) {
+            pm[j] = fmaxf(pm[j], __shfl_xor(pm[j], 16));
+            pm[j] = fmaxf(pm[j], __shfl_xor(pm[j], 32));
+            if (q == 0) s_gmax[w][16 * j + c16] = valid ? pm[j] : 0.0f;
+        }
+        __syncthreads();
+        const int MB = (a.M + 15) >> 4, w0 = (w / RT) * RT;
+#pragma unroll
+        for (int j = 0; j < TB; j++) {
+            float gm = s_gmax[w0][16 * j + c16];
+#pragma unroll
+            for (int k = 1; k < RT; k++) gm = fmaxf(gm, s_gmax[w0 + k][16 * j + c16]);
+            const float scale = quant_scale(gm, a.qflavor), inv = quant_inv(scale);
+            const int m = m0 + 16 * j + c16;
+            if (!valid || m >= a.M) continue;
+#pragma unroll
+            for (int i = 0; i < TA; i++) {
+                const uint32_t b0 = (uint8_t)quant_one(hv[i][j][0], scale, inv, a.qflavor);
+                const uint32_t b1 = (uint8_t)quant_one(hv[i][j][1], scale, inv, a.qflavor);
+                const int k0 = 8 * (tx * TA + i) + 4 * qq + 2 * half;
+                *(uint16_t *)(a.hq + pf_act_off(m, k0, MB)) = (uint16_t)(b0 | (b1 << 8));
+            }
+            if (w == w0 && q == 0) a.hsc[pf_scale_off(m, (8 * tx * TA) / 32, MB)] = scale;
         }
     }
 }
@@ -379,11 +454,28 @@ hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStre
         return hipErrorInvalidValue;
     const int shape = a.shape ? a.shape : pgemm_pick_shape(W.rows, a.M, a.simds);
     const int TA = shape / 10, TB = shape % 10;
+    if (a.swiglu) {
+        // gate/up in row-blocks of 8 + 8, whole quantization groups of 32 hidden values, int4 weights
+        if (wbits != 4 || W.rb != 16 || W.rows % 64 || ((uintptr_t)a.hq & 3) || ((uintptr_t)a.hsc & 3) ||
+            !a.hq || !a.hsc || (TA != 1 && TA != 2) || (TB != 1 && TB != 2))
+            return hipErrorInvalidValue;
+        const int RT = 4 / TA, NTY = 4 / RT;
+        const int xt = W.rows / (16 * TA), yt = (a.M + 16 * TB - 1) / (16 * TB);
+        const unsigned blocks = (unsigned)(8 * ((xt / RT + 7) / 8) * ((yt + NTY - 1) / NTY));
+#define PGS(TA_, TB_)                                                                                          \
+        if (TA == TA_ && TB == TB_) {                                                                         \
+            hipLaunchKernelGGL((k_pgemm<4, 32, 0, TA_, TB_, 1>), dim3(blocks), dim3(256), 0, st, a);         \
+            return hipGetLastError();                                                                         \
+        }
+        PGS(1, 1) PGS(1, 2) PGS(2, 1) PGS(2, 2)
+#undef PGS
+        return hipErrorInvalidValue;
+    }
 #define PGW(WB_, GS_, SF_, TA_, TB_)                                                                           \
     if (TA == TA_ && TB == TB_) {                                                                             \
         const int xt = (W.rows + 16 * TA_ - 1) / (16 * TA_), yt = (a.M + 16 * TB_ - 1) / (16 * TB_);          \
         const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * ((yt + 3) / 4));                              \
-        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_, TA_, TB_>), dim3(blocks), dim3(256), 0, st, a);           \
+        hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_, TA_, TB_, 0>), dim3(blocks), dim3(256), 0, st, a);        \
         return hipGetLastError();                                                                             \
     }
 #define PG(WB_, GS_, SF_)                                                                                      \

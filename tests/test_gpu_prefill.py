@@ -138,6 +138,28 @@ def test_prefill_equals_the_per_position_path_across_chunks(tmp_path):
     b.close()
 
 
+@pytest.mark.parametrize("n,strict", [(512, False), (40, False), (512, True)])
+def test_prefill_swiglu_epilogue_equals_the_separate_kernel(monkeypatch, tmp_path, n, strict):
+    """the gate/up GEMM's SwiGLU + int8 quantization epilogue against the separate SwiGLU kernel
+    (LLM_PF_SWIGLU=0): the same float operations in the same order, so the prefill logits and every layer's K/V
+    rows are bitwise equal (512 tokens: 32 x 32 tiles, two waves per quantization group; 40 tokens: 16 x 16
+    tiles, four waves, a partial token tile; and the strict mode, whose SiLU takes the reference's expf)"""
+    p = synth("qwb", str(tmp_path / "sw.qwb"), "c3", 41, "layers=2", "vocab=4096", "head_k=4096")
+    ids = [int(v) for v in np.random.default_rng(12).integers(0, 4096, n)]
+    runs = []
+    for setting in ("0", "1"):
+        monkeypatch.setenv("LLM_PF_SWIGLU", setting)
+        m = pkg().Model(p, 600)
+        if strict:
+            m.set_strict(True)
+        lg = m.prefill(ids)
+        runs.append((lg, kv_rows(m, n)))
+        m.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    for (ka, va), (kb, vb) in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
 def test_prefill_c3_shapes_two_layers(tmp_path):
     """Qwen2-0.5B layer shapes, two layers: prefill logits of a 40-token prompt against the oracle's forced
     prompt (flip-limited bar: see test_gpu_model.py)"""
