@@ -846,7 +846,21 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
     const int m = blockIdx.x, hs = a.head_size, S = (a.p0 + m) / a.att_sl + 1;
     if (S == 1 && !all) return;
     // fixed-trip loops with the slice count as a predicate: every load of a row is issued before the first
-    // is waited for
+    // is waited for.  The value partials of this thread's first MP outputs do not depend on the weights:
+    // they are loaded first, together with the statistics (one round trip for a row of up to MP * 256 values).
+    constexpr int MP = 4;
+    float xp[MP][PREFILL_ATT_SMAX];
+#pragma unroll
+    for (int p = 0; p < MP; p++) {
+        const int o = threadIdx.x + p * blockDim.x;
+        if (o < a.dim) {
+            const int h = o / hs, e = o - h * hs;
+            const float *acc = a.att_acc + ((size_t)m * a.n_heads + h) * a.att_smax * hs + e;
+#pragma unroll
+            for (int k = 0; k < PREFILL_ATT_SMAX; k++)
+                if (k < S) xp[p][k] = acc[(size_t)k * hs];
+        }
+    }
     for (int h = threadIdx.x; h < a.n_heads; h += blockDim.x) {
         const float *ml = a.att_ml + ((size_t)m * a.n_heads + h) * a.att_smax * 2;
         float mv[PREFILL_ATT_SMAX], lv[PREFILL_ATT_SMAX];
@@ -870,7 +884,19 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
             if (k < S) wgt[h * a.att_smax + k] = mv[k] * il;
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < a.dim; o += blockDim.x) {
+#pragma unroll
+    for (int p = 0; p < MP; p++) {
+        const int o = threadIdx.x + p * blockDim.x;
+        if (o < a.dim) {
+            const float *wh = wgt + (o / hs) * a.att_smax;
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < PREFILL_ATT_SMAX; k++)
+                if (k < S) v += xp[p][k] * wh[k];
+            row[o] = v;
+        }
+    }
+    for (int o = threadIdx.x + MP * blockDim.x; o < a.dim; o += blockDim.x) {
         const int h = o / hs, e = o - h * hs;
         const float *acc = a.att_acc + ((size_t)m * a.n_heads + h) * a.att_smax * hs + e;
         const float *wh = wgt + h * a.att_smax;
