@@ -101,6 +101,9 @@ struct llm_model {
     int8_t *pf_h = nullptr;
     float *pf_hs = nullptr;
     int pf_swiglu = 1;
+    // bias, RoPE and the q / K / V writes in the QKV GEMM's epilogue instead of k_p_qkv (LLM_PF_QKV=0 at
+    // llm_open: the separate kernel)
+    int pf_qkv = 1;
     // file mapping during load
     const uint8_t *file = nullptr;
     size_t file_size = 0;
@@ -528,6 +531,7 @@ int finish_setup(llm_model *m) {
     if (const char *e = getenv("LLM_WEIGHTS_NT")) m->weights_nt = m->head_nt = atoi(e) != 0; // 0 / 1: override
     if (const char *e = getenv("LLM_HEAD_NT")) m->head_nt = atoi(e) != 0;
     if (const char *e = getenv("LLM_PF_SWIGLU")) m->pf_swiglu = atoi(e) != 0;
+    if (const char *e = getenv("LLM_PF_QKV")) m->pf_qkv = atoi(e) != 0;
     return 0;
 }
 
@@ -902,6 +906,19 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     const int gu_shape = pgemm_pick_shape(m->L[0].gu.rows, M, g.simds);
     const bool fuse_swiglu = m->pf_swiglu && wb == 4 && m->gs == 32 && m->L[0].gu.rb == 16 &&
                              m->L[0].gu.rows % 64 == 0 && (gu_shape == 11 || gu_shape == 22);
+    // the QKV epilogue takes the 16 x 16 and 32 x 32 tiles
+    const int qkv_shape = pgemm_pick_shape(m->L[0].qkv.rows, M, g.simds);
+    const bool fuse_qkv = m->pf_qkv && (qkv_shape == 11 || qkv_shape == 22);
+    PgemmArgs gq = g;
+    gq.qkv = 1;
+    gq.rope_cos = m->rope_cos;
+    gq.rope_sin = m->rope_sin;
+    gq.q = m->pf_q;
+    gq.p0 = p0;
+    gq.dim = dim;
+    gq.kv_dim = kv;
+    gq.head_size = m->hs;
+    gq.rope_kind = pa.rope_kind;
     for (int l = 0; l < I.n_layers; l++) {
         const Layer &Ly = m->L[l];
         pa.kc = m->kc + (size_t)l * m->ctx * kv;
@@ -910,9 +927,17 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
         pa.norm_w = attn_norm(m, l);
         // after the first layer, the previous down projection's output (in y) joins x before the norm
         HIP_OR_FAIL("llm_prefill", launch_p_norm_quant(pa, l > 0, m->st));
-        g.W = Ly.qkv;
-        HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
-        HIP_OR_FAIL("llm_prefill", launch_p_qkv(pa, m->st));
+        if (fuse_qkv) {
+            gq.W = Ly.qkv;
+            gq.bias = pa.bias;
+            gq.kc = pa.kc;
+            gq.vc = pa.vc;
+            HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, gq, m->st));
+        } else {
+            g.W = Ly.qkv;
+            HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));
+            HIP_OR_FAIL("llm_prefill", launch_p_qkv(pa, m->st));
+        }
         HIP_OR_FAIL("llm_prefill", launch_p_attention(pa, m->st)); // the o projection's int8 input
         g.W = Ly.o;
         HIP_OR_FAIL("llm_prefill", launch_pgemm(wb, m->gs, sf, g, m->st));

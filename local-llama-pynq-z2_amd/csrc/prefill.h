@@ -46,6 +46,14 @@ struct PgemmArgs {
     int swiglu, qflavor, strict;
     int8_t *hq;             // pf_act_bytes(rows / 2, M); must not alias xq
     float *hsc;             // pf_scale_floats(rows / 64, M)
+    // qkv = 1: W is the fused QKV matrix (rows of q, then k, then v; NeoX: q and k in blocks of 16, 8 rows and
+    // their 8 RoPE partners) and the epilogue does k_p_qkv's work with the rows instead of storing y: bias,
+    // RoPE at position p0 + m, q rows to q [M][dim], K and V rows to the layer's caches (shapes 11 and 22)
+    int qkv;
+    const float *bias;      // [dim + 2 kv_dim] (NeoX) or NULL (interleaved pairs)
+    const float *rope_cos, *rope_sin; // [ctx][head_size / 2]
+    float *q, *kc, *vc;
+    int p0, dim, kv_dim, head_size, rope_kind;
 };
 
 // Tile shape of the prefill GEMM for d output rows and M tokens on a device of `simds` SIMDs.  The smallest

@@ -80,8 +80,11 @@ __device__ __forceinline__ void lane_row_transpose(uint32_t (&x)[4]) {
     x[3] = s23[1];
 }
 
-template <int WB, int GSZ, int SF32, int TA, int TB, int SWG>
+// EK: the epilogue: 0 stores y, 1 SwiGLU + quantization of h (PgemmArgs::swiglu), 2 bias + RoPE + the q / K / V
+// writes (PgemmArgs::qkv)
+template <int WB, int GSZ, int SF32, int TA, int TB, int EK>
 __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
+    constexpr bool SWG = EK == 1;
     constexpr int KC = GSZ / 32;             // 32-element chunks per group
     constexpr int AP = WB == 4 ? 1 : 2 * KC; // 16-byte pieces per (row, group) weight segment
     constexpr int GA = 4 / TA;               // groups per A load
@@ -338,6 +341,41 @@ __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
+    // QKV epilogue operands of every (row, token) of the tile: the bias of the row and of its RoPE partner
+    // (NeoX), and cos / sin at the token's position, loaded together in the epilogue.  (Loading them ahead of
+    // the weights costs the 16 x 16 tile a wave of occupancy, 106 -> 130 VGPRs, and measured slower: the
+    // 512-token Qwen2-0.5B-shape QKV GEMM 9.8 -> 10.6 us.)
+    [[maybe_unused]] float pb[TA][TB][4], pbp[TA][TB][4], pc[TA][TB][4], ps[TA][TB][4];
+    auto qkv_operands = [&]() __attribute__((always_inline)) {
+        const int dim = a.dim, hs = a.head_size, half = hs / 2, rot = dim + a.kv_dim;
+        const bool neox = a.rope_kind == ROPE_NEOX;
+#pragma unroll
+        for (int i = 0; i < TA; i++)
+#pragma unroll
+            for (int j = 0; j < TB; j++) {
+                const int m = min(m0 + 16 * j + c16, a.M - 1), pos = a.p0 + m;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int R = min(r0 + 16 * i + 4 * q + k, W.rows - 1), Rr = min(R, rot - 1);
+                    int ii, ib = R, ibp = R;
+                    if (neox) {
+                        const int blk = Rr / 16, r = Rr & 15, per = half / 8, hh = blk / per;
+                        ii = (blk - hh * per) * 8 + (r & 7);
+                        if (R < rot) {
+                            ib = hh * hs + (r < 8 ? ii : half + ii);
+                            ibp = hh * hs + (r < 8 ? half + ii : ii);
+                        }
+                        pb[i][j][k] = a.bias[ib];
+                        pbp[i][j][k] = a.bias[ibp];
+                    } else {
+                        const int e = Rr < dim ? Rr : Rr - dim;
+                        ii = (e % hs) / 2;
+                    }
+                    pc[i][j][k] = a.rope_cos[(size_t)pos * half + ii];
+                    ps[i][j][k] = a.rope_sin[(size_t)pos * half + ii];
+                }
+            }
+    };
     const bool partial = nq > nfull;
     int qs = 0;
     if (nfull > 0) {
@@ -370,7 +408,69 @@ __global__ void __launch_bounds__(256) k_pgemm(PgemmArgs a) {
             for (int ee = 0; ee < 4; ee++)
                 if (kk == k && ee == e) products(d[ee & 1], kk, ee, nullptr);
     }
-    if constexpr (!SWG) {
+    if constexpr (EK == 2) {
+        // k_p_qkv's operations on the tile (qwen.c:515-524 / runq.c:500-521): lane row k of row tile i holds row
+        // R = r0 + 16 i + 4 q + k of token m; its NeoX partner R ^ 8 (same block of 16) is lane row k of the lane
+        // l ^ 32, its interleaved partner R ^ 1 lane row k ^ 1 of this lane.  The bias and RoPE operands of
+        // every (row, token) are loaded before (qkv_operands), then the outputs computed in k_p_qkv's order.
+        const int dim = a.dim, kvd = a.kv_dim, hs = a.head_size, half = hs / 2, rot = dim + kvd;
+        const bool neox = a.rope_kind == ROPE_NEOX;
+        qkv_operands();
+        float part[TA][TB][4];
+#pragma unroll
+        for (int i = 0; i < TA; i++)
+#pragma unroll
+            for (int j = 0; j < TB; j++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    // the NeoX partner, from the lane across the halves (every lane takes part in the swap)
+                    const uint32_t vb = __float_as_uint(acc[i][j][k]);
+                    const auto sw = __builtin_amdgcn_permlane32_swap(vb, vb, false, false);
+                    part[i][j][k] = __uint_as_float((q >> 1) ? sw[0] : sw[1]);
+                }
+#pragma unroll
+        for (int i = 0; i < TA; i++)
+#pragma unroll
+            for (int j = 0; j < TB; j++) {
+                const int m = m0 + 16 * j + c16, pos = a.p0 + m;
+                if (m >= a.M) continue;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int R = r0 + 16 * i + 4 * q + k;
+                    if (R >= W.rows) continue;
+                    const float v = acc[i][j][k];
+                    if (neox) {
+                        if (R < rot) {
+                            const int blk = R / 16, r = R & 15, per = half / 8, hh = blk / per;
+                            const int ii = (blk - hh * per) * 8 + (r & 7);
+                            const bool first = r < 8;
+                            const int e = hh * hs + (first ? ii : half + ii);
+                            const float c = pc[i][j][k], sn = ps[i][j][k];
+                            const float self = v + pb[i][j][k], partner = part[i][j][k] + pbp[i][j][k];
+                            float o;
+                            if (first) { float t1 = self * c, t2 = partner * sn; o = t1 - t2; }
+                            else { float t1 = self * c, t2 = partner * sn; o = t1 + t2; }
+                            if (e < dim) a.q[(size_t)m * dim + e] = o;
+                            else a.kc[(size_t)pos * kvd + (e - dim)] = o;
+                        } else {
+                            a.vc[(size_t)pos * kvd + (R - rot)] = v + pb[i][j][k];
+                        }
+                    } else {
+                        if (R < rot) {
+                            const int e = R < dim ? R : R - dim;
+                            const float c = pc[i][j][k], sn = ps[i][j][k], partner = acc[i][j][k ^ 1];
+                            float o;
+                            if ((e & 1) == 0) { float t1 = v * c, t2 = partner * sn; o = t1 - t2; }
+                            else { float t1 = partner * sn, t2 = v * c; o = t1 + t2; }
+                            if (R < dim) a.q[(size_t)m * dim + e] = o;
+                            else a.kc[(size_t)pos * kvd + e] = o;
+                        } else {
+                            a.vc[(size_t)pos * kvd + (R - rot)] = v;
+                        }
+                    }
+                }
+            }
+    } else if constexpr (!SWG) {
 #pragma unroll
         for (int j = 0; j < TB; j++) {
             const int m = m0 + 16 * j + c16;
@@ -454,6 +554,26 @@ hipError_t launch_pgemm(int wbits, int gs, int sf32, const PgemmArgs &a, hipStre
         return hipErrorInvalidValue;
     const int shape = a.shape ? a.shape : pgemm_pick_shape(W.rows, a.M, a.simds);
     const int TA = shape / 10, TB = shape % 10;
+    if (a.qkv) {
+        // q, k and v rows (NeoX: with the bias, q and k in blocks of 16), shapes 11 and 22
+        const int rot = a.dim + a.kv_dim, half = a.head_size / 2;
+        if (W.rows != a.dim + 2 * a.kv_dim || a.head_size % 2 || !a.q || !a.kc || !a.vc || !a.rope_cos ||
+            !a.rope_sin || a.p0 < 0 || (TA != TB) || (TA != 1 && TA != 2) || a.swiglu ||
+            (a.rope_kind == ROPE_NEOX && (!a.bias || rot % 16 || half % 8)) ||
+            (a.rope_kind != ROPE_NEOX && a.rope_kind != ROPE_INTERLEAVED))
+            return hipErrorInvalidValue;
+        const int xt = (W.rows + 16 * TA - 1) / (16 * TA), yt = (a.M + 16 * TB - 1) / (16 * TB);
+        const unsigned blocks = (unsigned)(8 * ((xt + 7) / 8) * ((yt + 3) / 4));
+#define PGQ(WB_, GS_, SF_, T_)                                                                                 \
+        if (wbits == WB_ && gs == GS_ && sf32 == SF_ && TA == T_) {                                           \
+            hipLaunchKernelGGL((k_pgemm<WB_, GS_, SF_, T_, T_, 2>), dim3(blocks), dim3(256), 0, st, a);       \
+            return hipGetLastError();                                                                         \
+        }
+        PGQ(4, 32, 0, 1) PGQ(4, 32, 0, 2) PGQ(8, 32, 0, 1) PGQ(8, 32, 0, 2) PGQ(8, 32, 1, 1) PGQ(8, 32, 1, 2)
+        PGQ(8, 64, 1, 1) PGQ(8, 64, 1, 2)
+#undef PGQ
+        return hipErrorInvalidValue;
+    }
     if (a.swiglu) {
         // gate/up in row-blocks of 8 + 8, whole quantization groups of 32 hidden values, int4 weights
         if (wbits != 4 || W.rb != 16 || W.rows % 64 || ((uintptr_t)a.hq & 3) || ((uintptr_t)a.hsc & 3) ||

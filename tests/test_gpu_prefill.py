@@ -160,6 +160,34 @@ def test_prefill_swiglu_epilogue_equals_the_separate_kernel(monkeypatch, tmp_pat
         assert np.array_equal(ka, kb) and np.array_equal(va, vb)
 
 
+@pytest.mark.parametrize("fmt,n,strict", [("qwb", 512, False), ("qwb", 600, False), ("qwb", 40, True),
+                                          ("bin", 300, False), ("bin", 150, True)])
+def test_prefill_qkv_epilogue_equals_the_separate_kernel(monkeypatch, tmp_path, fmt, n, strict):
+    """bias, RoPE and the q / K / V writes in the QKV GEMM's epilogue against the separate kernel
+    (LLM_PF_QKV=0): the same float operations, so the prefill logits and every layer's K/V rows are bitwise
+    equal.  NeoX pairs (.qwb: a row's partner 8 rows away, in the lane across the halves of the MFMA tile)
+    and interleaved pairs (.bin: the adjacent row, in the same lane), one prefill chunk and two (600 tokens:
+    the second chunk's RoPE positions start at 512), and the strict mode"""
+    if fmt == "qwb":
+        p = synth("qwb", str(tmp_path / "q.qwb"), "c3", 51, "layers=2", "vocab=4096", "head_k=4096")
+    else:
+        p = synth("bin", str(tmp_path / "q.bin"), "tiny", 52, "dim=256", "heads=4", "kv_heads=2", "gs=64",
+                  "hidden=256", "layers=2", "vocab=512", "max_seq=700")
+    ids = [int(v) for v in np.random.default_rng(13).integers(0, 512 if fmt == "bin" else 4096, n)]
+    runs = []
+    for setting in ("0", "1"):
+        monkeypatch.setenv("LLM_PF_QKV", setting)
+        m = pkg().Model(p, 700)
+        if strict:
+            m.set_strict(True)
+        lg = m.prefill(ids)
+        runs.append((lg, kv_rows(m, n)))
+        m.close()
+    assert np.array_equal(runs[0][0], runs[1][0])
+    for (ka, va), (kb, vb) in zip(runs[0][1], runs[1][1]):
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
 def test_prefill_c3_shapes_two_layers(tmp_path):
     """Qwen2-0.5B layer shapes, two layers: prefill logits of a 40-token prompt against the oracle's forced
     prompt (flip-limited bar: see test_gpu_model.py)"""
