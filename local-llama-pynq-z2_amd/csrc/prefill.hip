@@ -640,13 +640,38 @@ __global__ void __launch_bounds__(256) k_p_embed(ProwArgs a) {
 template <bool RESID>
 __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     extern __shared__ __align__(16) float sv[]; // dim floats + 4 per wave
-    const int m = blockIdx.x, n = a.dim;
+    const int m = blockIdx.x, n = a.dim, nt = blockDim.x;
     float *x = a.x + (size_t)m * n;
+    const float *y = a.y + (size_t)m * n;
+    // the first NQ passes' loads (x, y and the gains) are issued before the first store: a store to x could
+    // alias y, so a load after it would wait for it; each thread keeps its elements and their order
+    constexpr int NQ = 4;
+    float xv[NQ], yv[NQ], gv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int i = min(threadIdx.x + k * nt, n - 1);
+        xv[k] = x[i];
+        if constexpr (RESID) yv[k] = y[i];
+        gv[k] = a.norm_w[i];
+    }
     float part = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int i = threadIdx.x + k * nt;
+        if (i < n) {
+            float v = xv[k];
+            if constexpr (RESID) {
+                v = v + yv[k];
+                x[i] = v;
+            }
+            sv[i] = v;
+            part += v * v;
+        }
+    }
+    for (int i = threadIdx.x + NQ * nt; i < n; i += nt) {
         float v = x[i];
         if constexpr (RESID) {
-            v = v + a.y[(size_t)m * n + i];
+            v = v + y[i];
             x[i] = v;
         }
         sv[i] = v;
@@ -664,7 +689,12 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     ss /= (float)n;
     ss += a.eps;
     ss = 1.0f / sqrtf(ss);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) sv[i] = a.norm_w[i] * (ss * sv[i]);
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int i = threadIdx.x + k * nt;
+        if (i < n) sv[i] = gv[k] * (ss * sv[i]);
+    }
+    for (int i = threadIdx.x + NQ * nt; i < n; i += nt) sv[i] = a.norm_w[i] * (ss * sv[i]);
     __syncthreads();
     block_quantize_tiles(sv, n, a.gs, a.qflavor, a.oq, a.os, m, pf_blocks(a.M));
 }
