@@ -69,6 +69,14 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
             iters = (T.nblocks + s.nb - 1) / s.nb;
         }
         s.grid = iters;
+        // Ordered sums: one row-block per block, so that a small matrix is spread over as many CUs as it has
+        // row-blocks (a CU pulls its block's bytes at a few tens of GB/s; the llama2.c 768/12L shapes: 12 ->
+        // 96 blocks for o and down, 2834 -> 3169 tok/s with 8-row blocks).  The SwiGLU epilogue's row-blocks
+        // per block are fixed by the quantization group.
+        if (s.ord && epi != EPI_SWIGLU) {
+            s.nb = 1;
+            s.grid = T.nblocks;
+        }
     }
     // The attention merge gives each thread one 4-value slot of the input: a block covers the whole input
     // in one pass (a second pass would read its operands after the weights are issued).
