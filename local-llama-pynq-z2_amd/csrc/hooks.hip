@@ -173,6 +173,7 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     float *dl = nullptr, *dp = nullptr;
     int *dr = nullptr;
     SamplerState *dss = nullptr;
+    void *dsc = nullptr; // the many-workgroup draw's buffers (taken for large n)
     SamplerState st;
     st.temperature = temperature;
     st.topp = topp;
@@ -181,6 +182,7 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     const size_t ld = ((size_t)n + 3) & ~(size_t)3; // 16-byte aligned rows
     if (hipMalloc(&dl, (size_t)count * ld * 4) == hipSuccess && hipMalloc(&dp, (size_t)n * 4) == hipSuccess &&
         hipMalloc(&dr, (size_t)count * 4) == hipSuccess && hipMalloc(&dss, sizeof st) == hipSuccess &&
+        hipMalloc(&dsc, sample_scratch_bytes()) == hipSuccess &&
         hipMemcpy2D(dl, ld * 4, logits, (size_t)n * 4, (size_t)n * 4, count, hipMemcpyHostToDevice) == hipSuccess &&
         hipMemcpy(dss, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess) {
         rc = 0;
@@ -192,6 +194,8 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
             a.probs = dp;
             a.ss = dss;
             a.out_row = dr + c;
+            a.scratch = dsc;
+            a.path = topp > 0.0f && topp < 1.0f ? 1 : 0;
             if (launch_sample(a, 0) != hipSuccess) rc = -1;
         }
         if (!rc && (hipDeviceSynchronize() != hipSuccess ||
@@ -205,6 +209,7 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     hipFree(dp);
     hipFree(dr);
     hipFree(dss);
+    hipFree(dsc);
     return rc;
 }
 

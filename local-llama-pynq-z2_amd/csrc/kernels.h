@@ -127,8 +127,14 @@ struct SampleArgs {
     int *pi;
     int np;
     int *out_row;           // optional: the sampled row
+    // the many-workgroup path's buffers (sample_scratch_bytes()), taken for n >= SMP_MULTI_MIN; NULL: the whole
+    // draw in one workgroup
+    void *scratch;
+    int path;               // many-workgroup path: the kernels launched, 0 the plain walk, 1 top-p, else both
+                            // (each returns at once unless the device-resident settings select it)
 };
 hipError_t launch_sample(const SampleArgs &a, hipStream_t st);
+size_t sample_scratch_bytes();
 
 struct RepackArgs {
     TiledMat T;             // output (T.data writable)

@@ -89,6 +89,8 @@ struct llm_model {
     bool sampling = false;
     SamplerState *ss = nullptr;
     float *smp_p = nullptr;
+    void *smp_scratch = nullptr; // the many-workgroup draw's buffers (large vocabularies)
+    int smp_path = -1;           // top-p (1) or the plain walk (0): the sampled step graphs launch that path only
     hipGraphExec_t g_plain_s = nullptr, g_hist_s = nullptr;
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
     int pf_cap = 0, prefill_on = 1;
@@ -203,6 +205,8 @@ hipError_t launch_sampler(llm_model *m) {
     a.pv = m->part_v;
     a.pi = m->part_i;
     a.np = m->s_head.grid;
+    a.scratch = m->smp_scratch;
+    a.path = m->smp_path;
     return launch_sample(a, m->st);
 }
 
@@ -1367,13 +1371,25 @@ extern "C" int llm_set_sampler(llm_model *m, float temperature, float topp, unsi
     hipSetDevice(m->device);
     HIP_OR_FAIL("llm_set_sampler", hipStreamSynchronize(m->st));
     const size_t n = (size_t)m->info.n_logits;
-    if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4))) return -1;
+    if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4) ||
+                   dalloc(m, (uint8_t **)&m->smp_scratch, sample_scratch_bytes())))
+        return -1;
     SamplerState st;
     st.temperature = temperature;
     st.topp = topp;
     st.rng = seed;
     HIP_OR_FAIL("llm_set_sampler", hipMemcpy(m->ss, &st, sizeof st, hipMemcpyHostToDevice));
     m->sampling = temperature > 0.0f; // the reference samples unless the temperature is 0 (qwen.c:647)
+    // the sampled step graphs hold one path's launches: captured again when the other one is set
+    const int path = topp > 0.0f && topp < 1.0f ? 1 : 0;
+    if (path != m->smp_path) {
+        for (hipGraphExec_t *g : {&m->g_plain_s, &m->g_hist_s})
+            if (*g) {
+                hipGraphExecDestroy(*g);
+                *g = nullptr;
+            }
+        m->smp_path = path;
+    }
     return 0;
 }
 

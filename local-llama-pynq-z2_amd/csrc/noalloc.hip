@@ -4,13 +4,14 @@
 // makes no hipMalloc, hipFree or other allocating call.
 //
 // The array is `scratch` below: staged logits (count rows of n rounded up to 4 floats, at most
-// NA_LOGITS floats), the probabilities of one row (n <= NA_PROBS), the sampled rows (count <= NA_ROWS) and the
-// sampler state.  Each GPU holds its own copy until the process ends.  Host code never uses the name
+// NA_LOGITS floats), the probabilities of one row (n <= NA_PROBS), the sampled rows (count <= NA_ROWS), the
+// sampler state and the buffers of the many-workgroup draw that mvh_sample takes for large n (so both entry
+// points draw alike).  Each GPU holds its own copy until the process ends.  Host code never uses the name
 // `scratch` as an address: its device address on each GPU is looked up once, with that GPU current, by
 // hipGetSymbolAddress, and only that address reaches copies and kernels.  Every call on one GPU shares the
 // array; calls that overlap on one GPU (other host threads) race.  Nothing in it has to start at zero: the
-// staged logits and the state are copied in before the kernels run, and the kernel writes every probability
-// and row it reads back.
+// staged logits and the state are copied in before the kernels run, and the kernels write every probability,
+// row and draw buffer before they read it back (the radix histograms are cleared by the draw's first kernel).
 #include <string.h>
 
 #include "../../include/llm_hip.h"
@@ -23,7 +24,9 @@ constexpr size_t NA_ROWS = 4096;              // sampled rows
 constexpr size_t OFF_PROBS = NA_LOGITS * 4;
 constexpr size_t OFF_ROWS = OFF_PROBS + NA_PROBS * 4;
 constexpr size_t OFF_STATE = OFF_ROWS + NA_ROWS * 4;
-constexpr size_t NA_BYTES = OFF_STATE + 256;
+constexpr size_t OFF_DRAW = OFF_STATE + 256;
+constexpr size_t NA_DRAW = (size_t)64 << 10; // the many-workgroup draw's buffers (sample_scratch_bytes())
+constexpr size_t NA_BYTES = OFF_DRAW + NA_DRAW;
 } // namespace
 
 static __device__ __align__(256) uint8_t scratch[NA_BYTES];
@@ -64,6 +67,11 @@ extern "C" int mvh_sample_noalloc(const float *logits, int n, int count, float t
                 "%zu logits in all)\n", who, count, n, NA_PROBS, NA_ROWS, NA_LOGITS);
         return -1;
     }
+    if (sample_scratch_bytes() > NA_DRAW) {
+        fprintf(stderr, "%s: internal error: the draw's buffers need %zu bytes, %zu reserved\n", who,
+                sample_scratch_bytes(), NA_DRAW);
+        return -1;
+    }
     const int dev = hip_device_from_env(who);
     if (dev < 0) return -1;
     HIP_OR_FAIL(who, hipSetDevice(dev));
@@ -86,6 +94,8 @@ extern "C" int mvh_sample_noalloc(const float *logits, int n, int count, float t
         a.probs = dp;
         a.ss = dss;
         a.out_row = dr + c;
+        a.scratch = s + OFF_DRAW;
+        a.path = topp > 0.0f && topp < 1.0f ? 1 : 0;
         HIP_OR_FAIL(who, launch_sample(a, 0));
     }
     HIP_OR_FAIL(who, hipStreamSynchronize(0));

@@ -138,6 +138,27 @@ def test_all_equal_logits_take_ties_in_index_order():
     assert got.max() <= 501  # the prefix passes topp = 0.5 after ~500 equal candidates
 
 
+def test_sampled_generation_over_a_large_vocabulary_matches_the_draws_of_the_same_logits(tmp_path):
+    """vocabularies of 8192 rows and more take the many-workgroup draw; inside the step graph it must draw
+    what sample() draws from the same logits and seed (sample() itself is held to the oracle above): the
+    generated ids are those rows mapped through head_ids.  Top-p, then the plain walk on the same model, then
+    top-p again (the sampled step graphs hold one path's launches and are captured again on a switch)"""
+    from helpers import synth
+    p = synth("qwb", str(tmp_path / "v.qwb"), "c3", 61, "layers=2", "vocab=16384", "head_k=16384")
+    m = pkg().Model(p, 128)
+    m.set_prefill(False)
+    prompt = [int(v) for v in np.random.default_rng(3).integers(0, 16384, 8)]
+    hid = np.asarray(m.head_ids)
+    for temp, topp, seed in ((0.8, 0.9, 77), (1.1, 1.0, 78), (0.6, 0.5, 79)):
+        m.set_sampler(temp, topp, seed)
+        r = m.generate(prompt, 12, logits=True)
+        ids = list(r["ids"])
+        lg = np.asarray(r["logits"])[len(prompt) - 1:len(prompt) - 1 + len(ids)]
+        rows, _ = pkg().sample(lg, temp, topp, seed)
+        assert [int(hid[k]) for k in rows] == ids, (temp, topp)
+    m.close()
+
+
 @pytest.mark.parametrize("name,prefill", [("qwb_sampled", True), ("qwb_sampled", False), ("qwb_sampled_mult", True),
                                           ("bin_sampled", True)])
 def test_sampled_generation_matches_reference_ids(name, prefill):
