@@ -100,7 +100,9 @@ def logit_sets(n, count, rng):
     return out
 
 
-@pytest.mark.parametrize("n", [256, 4097, 65536, 152064])
+# 256 and 4097 rows: one workgroup; 8192 and more: the many-workgroup draw (9999: a last chunk of 15 rows,
+# a last vector of 3)
+@pytest.mark.parametrize("n", [256, 4097, 8192, 9999, 65536, 152064])
 @pytest.mark.parametrize("topp", [0.0, 0.5, 0.9, 0.99, 1.0])
 def test_device_sampler_matches_oracle(n, topp):
     rng = np.random.default_rng(n * 7 + int(topp * 100))
