@@ -441,23 +441,31 @@ __device__ bool smb_select_state(const SampleArgs &a, const SmpScratch *S, int s
                                  u64 *t_out, u64 *total_out, unsigned *prefix, u64 *before) {
     static_assert(SMB_T == 256, "one radix bucket per thread");
     const int b = threadIdx.x;
+    // every level's bucket of this thread and the select's settings, loaded together
+    const u64 h0 = S->H[0][b];
+    u64 hv[4];
+#pragma unroll
+    for (int lvl = 1; lvl < 4; lvl++) hv[lvl] = lvl < levels ? S->H[3 * sel + lvl][b] : 0;
+    const int need_b = S->need_b;
+    const u64 rt = S->rt;
+    const float topp = a.ss->topp;
     u64 total;
-    const u64 pre0 = smb_excl_scan(S->H[0][b], sh, &total);
+    const u64 pre0 = smb_excl_scan(h0, sh, &total);
     *total_out = total;
     if (total == 0) return false;
     u64 t;
     if (sel == 0) {
-        const u64 tp = fixed_mass(a.ss->topp);
+        const u64 tp = fixed_mass(topp);
         t = tp < total ? tp : total - 1;
     } else {
-        if (!S->need_b) return false;
-        t = S->rt;
+        if (!need_b) return false;
+        t = rt;
     }
     *t_out = t;
     unsigned pr = 0;
     u64 bf = 0;
     for (int lvl = 0; lvl < levels; lvl++) {
-        const u64 h = lvl == 0 ? S->H[0][b] : S->H[3 * sel + lvl][b];
+        const u64 h = lvl == 0 ? h0 : hv[lvl];
         u64 lt;
         const u64 pre = lvl == 0 ? pre0 : smb_excl_scan(h, sh, &lt);
         if (lvl == 0) lt = total;
@@ -493,6 +501,52 @@ __device__ __forceinline__ void smb_flush(SmbShared &sh, u64 *global) {
 }
 
 __device__ __forceinline__ void smb_hist_add(SmbShared &sh, int b, u64 q) { atomicAdd((unsigned long long *)&sh.hist[b], (unsigned long long)q); }
+
+// The workgroup's rows of probabilities as float4 per lane: the first SMB_PF chunks of each wave, loaded before
+// the radix state is worked out (they do not depend on it); later chunks (large vocabularies) are loaded as used.
+#define SMB_PF 4
+struct SmbRows {
+    float4 v[SMB_PF];
+    int c0, c1;
+    __device__ __forceinline__ void load(const SampleArgs &a) {
+        smb_range(a.n, &c0, &c1);
+        const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+        for (int k = 0; k < SMB_PF; k++) {
+            const int c = c0 + w + k * (SMB_T / WAVE);
+            v[k] = smb_rows(a.probs, a.n, min(c, c1 - 1), lane);
+        }
+    }
+    // f(chunk, float4 of the lane) over the workgroup's chunks
+    template <typename F>
+    __device__ __forceinline__ void each(const SampleArgs &a, F f) const {
+        const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+        for (int k = 0; k < SMB_PF; k++) {
+            const int c = c0 + w + k * (SMB_T / WAVE);
+            if (c < c1) f(c, v[k]);
+        }
+        for (int c = c0 + w + SMB_PF * (SMB_T / WAVE); c < c1; c += SMB_T / WAVE) f(c, smb_rows(a.probs, a.n, c, lane));
+    }
+};
+
+// a thread's run of masses in one bucket, added to the LDS histogram once per run (rows of near-equal
+// probability share a bucket: one LDS atomic per row would serialize on it)
+struct SmbRun {
+    int b = -1;
+    u64 q = 0;
+    __device__ __forceinline__ void add(SmbShared &sh, int bucket, u64 mass) {
+        if (bucket != b) {
+            if (b >= 0) smb_hist_add(sh, b, q);
+            b = bucket;
+            q = 0;
+        }
+        q += mass;
+    }
+    __device__ __forceinline__ void end(SmbShared &sh) {
+        if (b >= 0) smb_hist_add(sh, b, q);
+    }
+};
 
 // the sampled row as the only finite entry of the argmax partials (as k_sample)
 __device__ __forceinline__ void smb_emit(const SampleArgs &a, int row) {
@@ -617,18 +671,28 @@ __global__ void __launch_bounds__(SMB_T) ks_probs(SampleArgs a) {
     SmpScratch *S = (SmpScratch *)a.scratch;
     const int n = a.n, lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const float temp = a.ss->temperature, topp = a.ss->topp;
-    // the maximum (first row on ties) and the sum, combined in workgroup order
-    if (threadIdx.x == 0) {
-        float gm = -INFINITY;
-        int mi = 0x7fffffff;
-        for (int b = 0; b < (int)gridDim.x; b++)
-            if (S->pm[b] > gm || (S->pm[b] == gm && S->pi[b] < mi)) { gm = S->pm[b]; mi = S->pi[b]; }
-        float sum = 0.0f;
-        for (int b = 0; b < (int)gridDim.x; b++)
-            if (S->pm[b] > -INFINITY) sum += S->ps[b] * expf(S->pm[b] - gm);
-        sh.bf[0] = gm;
-        sh.bf[1] = sum;
-        sh.bi[0] = mi == 0x7fffffff ? 0 : mi;
+    // the maximum (first row on ties) and the sum over the workgroups' partials, one per lane of wave 0 (the
+    // sum in a fixed butterfly order: every workgroup gets the same value)
+    static_assert(SMB_NB <= WAVE, "one partial per lane");
+    if (threadIdx.x < WAVE) {
+        const int b = threadIdx.x;
+        const bool ok = b < (int)gridDim.x;
+        const float pm = ok ? S->pm[b] : -INFINITY, ps = ok ? S->ps[b] : 0.0f;
+        const int pi = ok ? S->pi[b] : 0x7fffffff;
+        float gm = pm;
+        int mi = pi;
+        for (int o = 1; o < WAVE; o <<= 1) {
+            const float ov = __shfl_xor(gm, o);
+            const int oi = __shfl_xor(mi, o);
+            if (ov > gm || (ov == gm && oi < mi)) { gm = ov; mi = oi; }
+        }
+        float term = pm > -INFINITY ? ps * expf(pm - gm) : 0.0f;
+        for (int o = 1; o < WAVE; o <<= 1) term += __shfl_xor(term, o);
+        if (b == 0) {
+            sh.bf[0] = gm;
+            sh.bf[1] = term;
+            sh.bi[0] = mi == 0x7fffffff ? 0 : mi;
+        }
     }
     for (int b = threadIdx.x; b < 256; b += SMB_T) sh.hist[b] = 0;
     __syncthreads();
@@ -637,6 +701,7 @@ __global__ void __launch_bounds__(SMB_T) ks_probs(SampleArgs a) {
     const bool use_topp = topp > 0.0f && topp < 1.0f;
     int c0, c1;
     smb_range(n, &c0, &c1);
+    SmbRun run;
     for (int c = c0 + w; c < c1; c += SMB_T / WAVE) {
         const int i = c * SMP_CHUNK + 4 * lane;
         const float4 x = smb_rows(a.logits, n, c, lane);
@@ -646,8 +711,9 @@ __global__ void __launch_bounds__(SMB_T) ks_probs(SampleArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             pv[j] = i + j < n ? expf(xs[j] / temp - gm) / sum : 0.0f; // qwen.c:351
-            m += fixed_mass(pv[j]);
-            if (use_topp && i + j < n && pv[j] >= cutoff) smb_hist_add(sh, (~__float_as_uint(pv[j])) >> 24, fixed_mass(pv[j]));
+            const u64 q = fixed_mass(pv[j]);
+            m += q;
+            if (use_topp && i + j < n && pv[j] >= cutoff) run.add(sh, (~__float_as_uint(pv[j])) >> 24, q);
         }
         if (i + 3 < n) *(float4 *)(a.probs + i) = make_float4(pv[0], pv[1], pv[2], pv[3]);
         else
@@ -656,6 +722,7 @@ __global__ void __launch_bounds__(SMB_T) ks_probs(SampleArgs a) {
         const u64 cmass = wave_sum_u64(m);
         if (lane == 0) S->cm[c] = cmass;
     }
+    run.end(sh);
     if (use_topp) smb_flush(sh, S->H[0]);
     // the coin (qwen.c:638-645, 651), once per draw
     if (blockIdx.x == 0 && threadIdx.x == 0) {
@@ -676,26 +743,27 @@ __global__ void __launch_bounds__(SMB_T) ks_level(SampleArgs a, int sel, int lvl
     if (smb_forced(a)) return;
     if (!smb_use_topp(a)) return;
     SmpScratch *S = (SmpScratch *)a.scratch;
+    SmbRows rows;
+    rows.load(a);
     u64 t, total, before;
     unsigned prefix;
     if (!smb_select_state(a, S, sel, lvl, sh, &t, &total, &prefix, &before)) return;
     for (int b = threadIdx.x; b < 256; b += SMB_T) sh.hist[b] = 0;
     __syncthreads();
-    const int n = a.n, lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE, sh_b = 24 - 8 * lvl;
+    const int n = a.n, sh_b = 24 - 8 * lvl;
     const float cutoff = (1.0f - a.ss->topp) / (n - 1);
-    int c0, c1;
-    smb_range(n, &c0, &c1);
-    for (int c = c0 + w; c < c1; c += SMB_T / WAVE) {
-        const float4 v = smb_rows(a.probs, n, c, lane); // rows past n read 0: never a candidate
+    SmbRun run;
+    rows.each(a, [&](int, float4 v) { // rows past n read 0: never a candidate
         const float r4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             if (!(r4[j] >= cutoff)) continue;
             const unsigned key = ~__float_as_uint(r4[j]);
             if ((key >> (sh_b + 8)) != prefix) continue;
-            smb_hist_add(sh, (key >> sh_b) & 255, fixed_mass(r4[j]));
+            run.add(sh, (key >> sh_b) & 255, fixed_mass(r4[j]));
         }
-    }
+    });
+    run.end(sh);
     smb_flush(sh, S->H[3 * sel + lvl]);
 }
 
@@ -704,18 +772,17 @@ __global__ void __launch_bounds__(SMB_T) ks_ties(SampleArgs a, int sel) {
     __shared__ SmbShared sh;
     if (smb_forced(a) || !smb_use_topp(a)) return;
     SmpScratch *S = (SmpScratch *)a.scratch;
+    SmbRows rows;
+    rows.load(a);
     u64 t, total, before;
     unsigned prefix;
     if (!smb_select_state(a, S, sel, 4, sh, &t, &total, &prefix, &before)) return;
     const float pv = __uint_as_float(~prefix);
-    const int n = a.n, lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    int c0, c1;
-    smb_range(n, &c0, &c1);
-    for (int c = c0 + w; c < c1; c += SMB_T / WAVE) {
-        const float4 v = smb_rows(a.probs, n, c, lane); // rows past n read 0, which is never pv (pv >= cutoff > 0)
+    const int lane = threadIdx.x & (WAVE - 1);
+    rows.each(a, [&](int c, float4 v) { // rows past n read 0, which is never pv (pv >= cutoff > 0)
         const u64 cnt = wave_sum_u64((u64)((int)(v.x == pv) + (int)(v.y == pv) + (int)(v.z == pv) + (int)(v.w == pv)));
         if (lane == 0) S->tc[c] = cnt;
-    }
+    });
 }
 
 // the end of a draw (one workgroup): plain walk (sel < 0) or the end of top-p select `sel`
