@@ -425,7 +425,7 @@ __device__ __forceinline__ void smb_range(int n, int *c0, int *c1) {
     *c1 = min(*c0 + per, nc);
 }
 
-// the probability of row i and whether it exists (rows past n: 0)
+// the lane's four probabilities of chunk c (rows past n read 0)
 __device__ __forceinline__ float4 smb_rows(const float *x, int n, int c, int lane) { return chunk_rows(x, n, c, lane); }
 
 __device__ __forceinline__ bool smb_use_topp(const SampleArgs &a) { return a.ss->topp > 0.0f && a.ss->topp < 1.0f; }
