@@ -106,6 +106,9 @@ struct llm_model {
     // bias, RoPE and the q / K / V writes in the QKV GEMM's epilogue instead of k_p_qkv (LLM_PF_QKV=0 at
     // llm_open: the separate kernel)
     int pf_qkv = 1;
+    // the prefill attention's products on bf16 MFMA over three-piece splits of the fp32 operands
+    // (LLM_PF_FLASH_BF=0 at llm_open: fp32 MFMA)
+    int pf_flash_bf = 1;
     // file mapping during load
     const uint8_t *file = nullptr;
     size_t file_size = 0;
@@ -536,6 +539,7 @@ int finish_setup(llm_model *m) {
     if (const char *e = getenv("LLM_HEAD_NT")) m->head_nt = atoi(e) != 0;
     if (const char *e = getenv("LLM_PF_SWIGLU")) m->pf_swiglu = atoi(e) != 0;
     if (const char *e = getenv("LLM_PF_QKV")) m->pf_qkv = atoi(e) != 0;
+    if (const char *e = getenv("LLM_PF_FLASH_BF")) m->pf_flash_bf = atoi(e) != 0;
     return 0;
 }
 
@@ -895,6 +899,7 @@ int prefill_chunk(llm_model *m, const int *ids, int p0, int M) {
     pa.att_ml = m->pf_ml;
     pa.att_acc = m->pf_acc;
     pa.strict = m->strict;
+    pa.flash_bf = m->pf_flash_bf;
     pa.xb = m->pf_y; // strict attention rows: the QKV GEMM output is consumed by then
     HIP_OR_FAIL("llm_prefill", launch_p_embed(pa, m->st));
     PgemmArgs g;

@@ -90,6 +90,7 @@ struct ProwArgs {           // per-token elementwise kernels
     // ml [M][n_heads][att_smax][2] (max, sum of exp) and acc [M][n_heads][att_smax][hs]
     int att_sl, att_smax;
     float *att_ml, *att_acc;
+    int flash_bf;           // 1: the slice kernel's products on bf16 MFMA over split operands (head sizes % 32 == 0)
 };
 
 // Slices of at least 64 positions, at most 16 per token for a chunk ending at position `end`.

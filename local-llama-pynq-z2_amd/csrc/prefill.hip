@@ -805,11 +805,55 @@ __host__ __device__ constexpr int pa_kc(int hs) { return hs >= 128 ? 32 : 64; }
 // With `direct`, a token whose positions all fall in slice 0 gets its output here, normalized and quantized
 // to int8 for the o projection (a group of gs values lies inside one head: hs % gs == 0); every other token
 // leaves its slice partials for k_p_attn_merge.
-template <int HS>
+//
+// BF (head sizes that are multiples of 32): the same products on `v_mfma_f32_16x16x32_bf16`.  Every fp32 operand
+// is split into three bf16 pieces, x = hi + mid + lo exactly (each piece the round-to-nearest of the remainder:
+// 8 significant bits each, with the remainder exact in fp32), and a product takes the six piece products whose
+// size is at least 2^-16 of it (hh, hm, mh, hl, lh, mm, smallest first); what is left out is below 2^-24 of
+// the product, the order of fp32 rounding.  bf16 products are exact in fp32.  A and B lanes pair the same
+// 8 terms (lane group g, slot j), so the layouts are:
+//   scores: K rows staged as three bf16 planes [key][HS + 8]; slot j of chunk c is dim g * HS/4 + 8c + j;
+//   values: V staged transposed, three planes [dim][PA_KC + 8], keys of a 32-key chunk stored in the order
+//     of the probability lanes (slot j < 4: key 4g + j of the chunk's first 16, j >= 4: of its second 16).
+typedef __bf16 pa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float pa_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 pa_bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t pa_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t pa_bf2(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((pa_f32x2){x, y}, pa_bf16x2));
+}
+// (x, y) = p[0] + p[1] + p[2], each word a pair of bf16 (x in the low half)
+__device__ __forceinline__ void pa_split3(float x, float y, uint32_t *p) {
+    p[0] = pa_bf2(x, y);
+    const float x1 = x - __uint_as_float(p[0] << 16), y1 = y - __uint_as_float(p[0] & 0xffff0000u);
+    p[1] = pa_bf2(x1, y1);
+    p[2] = pa_bf2(x1 - __uint_as_float(p[1] << 16), y1 - __uint_as_float(p[1] & 0xffff0000u));
+}
+__device__ __forceinline__ pa_bf16x8 pa_bf8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(pa_bf16x8, (pa_u32x4){a, b, c, d});
+}
+// d += A . B over the split operands (pieces h, m, l), smallest products first
+__device__ __forceinline__ f32x4v pa_mfma6(const pa_bf16x8 (&A)[3], const pa_bf16x8 (&B)[3], f32x4v d) {
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1], B[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], B[2], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[2], B[0], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], B[1], d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[1], B[0], d, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[0], B[0], d, 0, 0, 0);
+}
+__host__ __device__ constexpr size_t pa_lds_bytes(int hs, int bf) {
+    return bf ? (size_t)2 * 3 * ((size_t)pa_kc(hs) * (hs + 8) + (size_t)hs * (pa_kc(hs) + 8))
+              : (size_t)2 * pa_kc(hs) * (hs + 4) * 4;
+}
+
+template <int HS, int BF>
 __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
     constexpr int H4 = HS / 4, KS = HS + 4, DT = HS / 16, PA_KC = pa_kc(HS);
+    constexpr int KSB = HS + 8, VSB = PA_KC + 8, NCH = HS / 32; // BF: plane strides (bf16), dim chunks
+    static_assert(!BF || (HS % 32 == 0 && PA_KC % 32 == 0), "split-bf16 products take 32-element chunks");
     extern __shared__ __align__(16) float sm[];
     float *sk = sm, *sv = sm + PA_KC * KS; // [PA_KC][KS] each
+    uint16_t *skb = (uint16_t *)sm, *svb = skb + 3 * PA_KC * KSB; // BF: [3][PA_KC][KSB], [3][HS][VSB]
     const int kvh = blockIdx.x, m0 = 16 * blockIdx.y, s = blockIdx.z, kv_mul = a.n_heads / a.n_kv;
     const int t_begin = s * a.att_sl;
     const int t_stop = min(t_begin + a.att_sl, a.p0 + min(m0 + 16, a.M)); // keys of the slice any token sees
@@ -831,6 +875,17 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
             qv[4 * i + 3] = v.w;
         }
     }
+    pa_bf16x8 qb[BF ? NCH : 1][3]; // BF: the query's pieces, chunk c slot j = qv[8c + j]
+    if constexpr (BF) {
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            uint32_t w[4][3];
+#pragma unroll
+            for (int j = 0; j < 4; j++) pa_split3(qv[8 * c + 2 * j], qv[8 * c + 2 * j + 1], w[j]);
+#pragma unroll
+            for (int p = 0; p < 3; p++) qb[c][p] = pa_bf8(w[0][p], w[1][p], w[2][p], w[3][p]);
+        }
+    }
     f32x4v o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -844,8 +899,27 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
             const int k = i / H4, c = i - k * H4;
             const size_t gi = (size_t)(tc + min(k, nk - 1)) * a.kv_dim + (size_t)kvh * HS + 4 * c;
             const f32x4v kk = *(const f32x4v *)(a.kc + gi), vv = *(const f32x4v *)(a.vc + gi);
-            *(f32x4v *)(sk + k * KS + 4 * c) = kk;
-            *(f32x4v *)(sv + k * KS + 4 * c) = vv;
+            if constexpr (BF) {
+                uint32_t k0[3], k1[3], v0[3], v1[3];
+                pa_split3(kk.x, kk.y, k0);
+                pa_split3(kk.z, kk.w, k1);
+                pa_split3(vv.x, vv.y, v0);
+                pa_split3(vv.z, vv.w, v1);
+                // the key's slot in its 32-key chunk: lane group g = (k % 16) / 4 holds slots 8g .. 8g + 7
+                const int kk32 = k & 31, kp = (k & ~31) + ((kk32 & 15) >> 2) * 8 + (kk32 >> 4) * 4 + (kk32 & 3);
+#pragma unroll
+                for (int p = 0; p < 3; p++) {
+                    *(uint2 *)(skb + (p * PA_KC + k) * KSB + 4 * c) = make_uint2(k0[p], k1[p]);
+                    uint16_t *vt = svb + (p * HS + 4 * c) * VSB + kp;
+                    vt[0] = (uint16_t)v0[p];
+                    vt[VSB] = (uint16_t)(v0[p] >> 16);
+                    vt[2 * VSB] = (uint16_t)v1[p];
+                    vt[3 * VSB] = (uint16_t)(v1[p] >> 16);
+                }
+            } else {
+                *(f32x4v *)(sk + k * KS + 4 * c) = kk;
+                *(f32x4v *)(sv + k * KS + 4 * c) = vv;
+            }
         }
         __syncthreads();
         const int ntile = (nk + 15) / 16;
@@ -856,14 +930,26 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
             sc[kt] = f32x4v{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             if (kt < ntile) {
                 f32x4v d = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
-                const float *kr = sk + (16 * kt + r) * KS + g * H4;
+                if constexpr (BF) {
 #pragma unroll
-                for (int i = 0; i < H4 / 4; i++) {
-                    const f32x4v kk = *(const f32x4v *)(kr + 4 * i);
-                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qv[4 * i], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qv[4 * i + 1], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qv[4 * i + 2], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qv[4 * i + 3], d, 0, 0, 0);
+                    for (int c = 0; c < NCH; c++) {
+                        pa_bf16x8 kb[3];
+#pragma unroll
+                        for (int p = 0; p < 3; p++)
+                            kb[p] = __builtin_bit_cast(
+                                pa_bf16x8, *(const pa_u32x4 *)(skb + (p * PA_KC + 16 * kt + r) * KSB + g * H4 + 8 * c));
+                        d = pa_mfma6(kb, qb[c], d);
+                    }
+                } else {
+                    const float *kr = sk + (16 * kt + r) * KS + g * H4;
+#pragma unroll
+                    for (int i = 0; i < H4 / 4; i++) {
+                        const f32x4v kk = *(const f32x4v *)(kr + 4 * i);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.x, qv[4 * i], d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.y, qv[4 * i + 1], d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.z, qv[4 * i + 2], d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(kk.w, qv[4 * i + 3], d, 0, 0, 0);
+                    }
                 }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -895,15 +981,42 @@ __global__ void __launch_bounds__(512) k_p_flash(ProwArgs a, int direct) {
 #pragma unroll
             for (int kt = 0; kt < PA_KC / 16; kt++) sc[kt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        if constexpr (BF) {
+            // chunk ch = tiles 2ch, 2ch + 1 (a tile past ntile has probabilities 0 and finite staged rows)
 #pragma unroll
-        for (int kt = 0; kt < PA_KC / 16; kt++) {
-            if (kt < ntile) {
+            for (int ch = 0; ch < PA_KC / 32; ch++) {
+                if (2 * ch < ntile) {
+                    uint32_t w[4][3];
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    const float *vr = sv + (16 * kt + 4 * g + u) * KS + r;
+                    for (int j = 0; j < 2; j++) {
+                        pa_split3(sc[2 * ch][2 * j], sc[2 * ch][2 * j + 1], w[j]);
+                        pa_split3(sc[2 * ch + 1][2 * j], sc[2 * ch + 1][2 * j + 1], w[2 + j]);
+                    }
+                    pa_bf16x8 pb[3];
 #pragma unroll
-                    for (int dt = 0; dt < DT; dt++)
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * dt], sc[kt][u], o[dt], 0, 0, 0);
+                    for (int p = 0; p < 3; p++) pb[p] = pa_bf8(w[0][p], w[1][p], w[2][p], w[3][p]);
+#pragma unroll
+                    for (int dt = 0; dt < DT; dt++) {
+                        pa_bf16x8 vb[3];
+#pragma unroll
+                        for (int p = 0; p < 3; p++)
+                            vb[p] = __builtin_bit_cast(
+                                pa_bf16x8, *(const pa_u32x4 *)(svb + (p * HS + 16 * dt + r) * VSB + 32 * ch + 8 * g));
+                        o[dt] = pa_mfma6(vb, pb, o[dt]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < PA_KC / 16; kt++) {
+                if (kt < ntile) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const float *vr = sv + (16 * kt + 4 * g + u) * KS + r;
+#pragma unroll
+                        for (int dt = 0; dt < DT; dt++)
+                            o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * dt], sc[kt][u], o[dt], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -1131,11 +1244,12 @@ hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
     const int direct = flash && hs % a.gs == 0 && (a.gs == 32 || a.gs == 64);
     if (flash) {
         const dim3 grid(a.n_kv, (a.M + 15) / 16, a.att_smax);
-        const size_t lds = (size_t)2 * pa_kc(hs) * (hs + 4) * 4;
-#define PF_FLASH(HS_)                                                                                         \
-    if (hs == HS_) hipLaunchKernelGGL(k_p_flash<HS_>, grid, dim3(64 * kv_mul), lds, st, a, direct);
-        PF_FLASH(16) PF_FLASH(32) PF_FLASH(48) PF_FLASH(64) PF_FLASH(128)
-#undef PF_FLASH
+        const int bf = a.flash_bf && hs % 32 == 0;
+        void (*kern)(ProwArgs, int) = nullptr;
+        if (bf) kern = hs == 32 ? k_p_flash<32, 1> : hs == 64 ? k_p_flash<64, 1> : k_p_flash<128, 1>;
+        else kern = hs == 16 ? k_p_flash<16, 0> : hs == 32 ? k_p_flash<32, 0> : hs == 48 ? k_p_flash<48, 0>
+                  : hs == 64 ? k_p_flash<64, 0> : k_p_flash<128, 0>;
+        hipLaunchKernelGGL(kern, grid, dim3(64 * kv_mul), pa_lds_bytes(hs, bf), st, a, direct);
     } else {
         hipLaunchKernelGGL(k_p_attention, dim3(a.n_kv, a.M, a.att_smax), dim3(256),
                            attn_lds_floats(kv_mul, hs) * 4, st, a);

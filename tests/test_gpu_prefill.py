@@ -225,3 +225,43 @@ def test_prefill_attention_head_shapes(tmp_path, fmt, shape, n):
     a.close()
     b.close()
     assert rel_err(lg_pf, lg_fw) < TOL
+
+
+@pytest.mark.parametrize("shape", [("dim=256", "heads=8", "kv_heads=2"), ("dim=512", "heads=8", "kv_heads=2"),
+                                   ("dim=512", "heads=4", "kv_heads=2")])
+def test_prefill_split_bf16_attention_against_the_fp32_products(monkeypatch, tmp_path, shape):
+    """head sizes 32, 64 and 128: the slice kernel's products on bf16 MFMA over three-piece splits of the fp32
+    operands (the default) and on fp32 MFMA (LLM_PF_FLASH_BF=0), two layers, a 200-token prompt (four slices of
+    64 positions), each against as many decode steps.  Layer 0's K/V rows come before any attention and are
+    bitwise equal in both modes.  After that the paths differ from the decode path where an activation
+    re-quantized after different fp32 sum orders crossed an int8 boundary: the logits and layer 1's rows are
+    held to the flip-limited bar of test_gpu_model.py in both modes, and the split products may not move more
+    of layer 1's positions than the fp32 products do (twice as many, plus a few: the counts are small).  The
+    one-layer logits bar (1e-3) for the split products is test_prefill_attention_head_shapes."""
+    extra = ["hidden=256", "layers=2", "vocab=512", "max_seq=256", "head_k=256"]
+    p = synth("qwb", str(tmp_path / "bf.qwb"), "tiny", 17, *shape, *extra)
+    b = pkg().Model(p, 256)
+    hid = b.head_ids
+    ids = [int(hid[v]) for v in np.random.default_rng(21).integers(0, len(hid), 200)]
+    for pos, t in enumerate(ids):
+        lg_fw = b.forward(t, pos)
+    rows_fw = kv_rows(b, 200)
+    b.close()
+    lg, rows, flips = {}, {}, {}
+    for bf in ("0", "1"):
+        monkeypatch.setenv("LLM_PF_FLASH_BF", bf)
+        m = pkg().Model(p, 256)
+        lg[bf] = m.prefill(ids)
+        rows[bf] = kv_rows(m, 200)
+        m.close()
+        assert rel_err(lg[bf], lg_fw) < 2e-2, bf
+        kv = len(rows[bf][0][0]) // 200
+        (ka, va), (kb, vb) = rows[bf][1], rows_fw[1]
+        e = np.maximum(np.abs(ka - kb).reshape(200, kv).max(1) / np.abs(kb).reshape(200, kv).max(1),
+                       np.abs(va - vb).reshape(200, kv).max(1) / np.abs(vb).reshape(200, kv).max(1))
+        assert e.max() < 2e-2, (bf, e.max())
+        flips[bf] = int((e > 1e-4).sum())
+    print("layer-1 positions moved past 1e-4 (fp32, split):", flips["0"], flips["1"])
+    for x, y in zip(rows["0"][0], rows["1"][0]):
+        assert np.array_equal(x, y)
+    assert flips["1"] <= 2 * flips["0"] + 6, flips
