@@ -7,10 +7,11 @@ greedy, batch 1.  A step is one decode position: the whole forward() plus the ar
 hipGraph replay.  `value` = timed steps / wall time between two device-wide synchronizations.
 
   python bench.py [--gpus 1] [--steps 128] [--warmup 8] [--config c1|c2|c3|c4|c5] [--no-cpu] [--no-counters]
-                  [--no-c5] [--no-strict]
+                  [--no-c5] [--no-c4] [--no-strict]
   python bench.py --traffic-from D --traffic-all     (every kernel kind's HBM bytes per launch from the passes in D)
   python bench.py --trace-summary T.csv              (a rocprofv3 kernel trace grouped by kernel and grid)
-  The default run (c3) also measures the Qwen2-7B shape (c5) and reports it as the sub-record "c5".
+  The default run (c3) also measures the Qwen2-7B shape (c5) and the 512-token batched prefill of its own model
+  (c4), and reports them as the sub-records "c5" and "c4".
   roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes that the
   run starts itself as child processes (FETCH_SIZE, then WRITE_SIZE, over `bench.py --counters`: a calibration
   copy of 1 GiB, then the prompt and 4 decode steps as eager launches), or from earlier passes:
@@ -267,12 +268,13 @@ def layer_macs(info):
     return info.n_layers * info.dim * (info.dim + 2 * kv + info.dim + 3 * info.hidden_dim)
 
 
-def prefill_bench(a, cfg, path, prompt):
-    """C4: the prompt as one batched prefill, timed over `steps` repetitions; int8 ops counted on the layer GEMMs"""
+def prefill_bench(a, cfg, path, prompt, reps=None):
+    """C4: the prompt as one batched prefill, timed over `reps` (else `steps`) repetitions; int8 ops counted on
+    the layer GEMMs.  Returns the record."""
     import torch
     P = load_pkg()
     m = P.Model(path, cfg["ctx"])
-    reps = a.steps or 5
+    reps = reps or a.steps or 5
     m.prefill(prompt)  # warmup (and the activation buffers)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -298,7 +300,7 @@ def prefill_bench(a, cfg, path, prompt):
                      "frac": round(ops / wall / 1e12 / PEAK_I8, 5), "traffic": None,
                      "note": "int8 ops of the layer GEMMs over the whole prefill time (every kernel included)"},
     }
-    print(json.dumps(out), flush=True)
+    return out
 
 
 def prompt_for(cfg, path):
@@ -464,6 +466,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="no reference runs (parity lines, CPU baseline)")
     ap.add_argument("--no-counters", action="store_true", help="no rocprofv3 counter passes (roofline.traffic null)")
     ap.add_argument("--no-c5", action="store_true", help="no Qwen2-7B-shape sub-record in the default run")
+    ap.add_argument("--no-c4", action="store_true", help="no 512-token prefill sub-record in the default run")
     ap.add_argument("--no-strict", action="store_true",
                     help="no strict-mode run after the fast mode (profiles of the fast mode's kernels alone)")
     ap.add_argument("--strict", action="store_true",
@@ -514,7 +517,8 @@ def main():
         return
     if a.config == "c4":
         path = model_file(cfg)
-        return prefill_bench(a, cfg, path, prompt_for(cfg, path))
+        print(json.dumps(prefill_bench(a, cfg, path, prompt_for(cfg, path))), flush=True)
+        return
     out = measure(a, a.config, steps, a.warmup, a.profile_steps, a.cpu_tokens or cfg["new"], not a.no_counters)
     if a.config == "c3" and not a.no_c5:
         # the 7B-shape configuration, whose GEMVs carry the HBM roofline target: a shorter record
@@ -522,6 +526,14 @@ def main():
         for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "data"):
             c5.pop(k, None)
         out["c5"] = c5
+    if a.config == "c3" and not a.no_c4:
+        # the batched prefill of a 512-token prompt on the same model (int8 MFMA GEMMs): a short record
+        c4cfg = CONFIGS["c4"]
+        p4 = model_file(c4cfg)
+        c4 = prefill_bench(a, c4cfg, p4, prompt_for(c4cfg, p4), reps=10)
+        for k in ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "data"):
+            c4.pop(k, None)
+        out["c4"] = c4
     print(json.dumps(out), flush=True)
 
 
