@@ -807,10 +807,10 @@ __host__ __device__ constexpr int pa_kc(int hs) { return hs >= 128 ? 32 : 64; }
 // leaves its slice partials for k_p_attn_merge.
 //
 // BF (head sizes that are multiples of 32): the same products on `v_mfma_f32_16x16x32_bf16`.  Every fp32 operand
-// is split into three bf16 pieces, x = hi + mid + lo exactly (each piece the round-to-nearest of the remainder:
-// 8 significant bits each, with the remainder exact in fp32), and a product takes the six piece products whose
-// size is at least 2^-16 of it (hh, hm, mh, hl, lh, mm, smallest first); what is left out is below 2^-24 of
-// the product, the order of fp32 rounding.  bf16 products are exact in fp32.  A and B lanes pair the same
+// is split into three bf16 pieces, x = hi + mid + lo exactly (each piece the round-to-nearest of what is left:
+// 8 significant bits, |mid| <= 2^-9 |x|, |lo| <= 2^-18 |x|, every remainder exact in fp32), and a product takes
+// six piece products (mm, hl, lh, hm, mh, hh: smallest first); the three left out (ml, lm, ll) are below
+// 2^-25 of the product, under fp32 rounding.  bf16 products are exact in fp32.  A and B lanes pair the same
 // 8 terms (lane group g, slot j), so the layouts are:
 //   scores: K rows staged as three bf16 planes [key][HS + 8]; slot j of chunk c is dim g * HS/4 + 8c + j;
 //   values: V staged transposed, three planes [dim][PA_KC + 8], keys of a 32-key chunk stored in the order
