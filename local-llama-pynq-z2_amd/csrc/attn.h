@@ -8,6 +8,7 @@
 #include "device.h"
 #include "kernels.h"
 #include "ref_expf.h"
+#include "seqsum.h"
 
 #ifndef KERNEL_MARK
 #define KERNEL_MARK(k)
@@ -145,13 +146,15 @@ __device__ __forceinline__ void attn_range(const float *q, const float *kc, cons
 // Block-wide (barriers inside); every thread of the block calls it.  sm: attn_strict_lds_floats floats.
 
 __host__ __device__ inline size_t attn_strict_lds_floats(int hs, int P, int threads) {
-    return (size_t)hs + (size_t)P + (size_t)threads / WAVE + 4;
+    return (size_t)hs + (((size_t)P + 3) & ~(size_t)3) + (((size_t)threads / WAVE + 4 + 3) & ~(size_t)3) +
+           seq_sum_scratch_bytes(threads) / 4 + 4;
 }
 
 __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc, const float *vc, int kv_dim,
                                                  int koff, int hs, int P, float *sm, float *out) {
     const int tid = threadIdx.x, nt = blockDim.x, lane = tid & (WAVE - 1), wave = tid / WAVE, nw = nt / WAVE;
-    float *sq = sm, *sc = sm + hs, *sred = sc + P;
+    float *sq = sm, *sc = sm + hs, *sred = sc + ((P + 3) & ~3);
+    uint8_t *sscr = (uint8_t *)(sred + ((nw + 4 + 3) & ~3)); // the sequential sum's scratch (16-byte aligned)
     for (int i = tid; i < hs; i += nt) sq[i] = q[i];
     __syncthreads();
     const float rs = sqrtf((float)hs);
@@ -176,9 +179,7 @@ __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc
     for (int w = 0; w < nw; w++) mx = fmaxf(mx, sred[w]);
     for (int t = tid; t < P; t += nt) sc[t] = ref_expf(sc[t] - mx);
     __syncthreads();
-    if (tid == 0) sred[nw] = seq_sum(sc, P);
-    __syncthreads();
-    const float sum = sred[nw];
+    const float sum = block_seq_sum<false>(sc, P, sscr);
     for (int t = tid; t < P; t += nt) sc[t] = sc[t] / sum;
     __syncthreads();
     for (int e = tid; e < hs; e += nt) {

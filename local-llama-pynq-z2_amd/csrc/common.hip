@@ -1,6 +1,8 @@
 // Launch-shape choice for the GEMV kernels and the bounded stream wait (internal).
 #include <time.h>
 
+#include <algorithm>
+
 #include "host_common.h"
 
 // Shapes follow from the tiled matrix: a row-block has `nchunks` chunk records of 1 KiB+ each; its chunks are
@@ -27,6 +29,9 @@ static void gemv_split(GemvShape &s, int C, int per_wave, const TiledMat &T, int
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus) {
     GemvShape s;
     const int C = T.nchunks;
+    // bit 1: the RMSNorm prologue sums sequentially (strict mode): its block-wide sum runs one segment per wave
+    const int seq_norm = (ordered & 2) && pro == PRO_NORM;
+    ordered &= 1;
     if (cus < 1) cus = 1;
     s.ord = 0;
     if (ordered) {
@@ -92,6 +97,15 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     // in one pass (a second pass would read its operands after the weights are issued).
     if (pro == PRO_ATTN)
         while (s.kw * s.nb * 64 < T.n / 4 && s.kw * s.nb < 16 && s.kw < C) s.kw++;
+    // the strict RMSNorm's sequential sum takes one segment per wave: at least 8 waves where the chunks allow,
+    // a persistent grid shrinking to what then fits at once
+    if (seq_norm) {
+        const int iters_now = (T.nblocks + s.nb - 1) / s.nb;
+        const bool persistent = s.grid < iters_now;
+        while (s.kw * s.nb < 8 && s.kw < C) s.kw++;
+        const int w = s.kw * s.nb;
+        if (persistent) s.grid = std::min(iters_now, cus * (w < 16 ? 16 / w : 1));
+    }
     if (s.grid < 1) s.grid = 1;
     s.depth = 2;
     return s;

@@ -101,33 +101,6 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
     return t;
 }
 
-// The reference's RMSNorm sum (qwen.c:337-339, runq.c:394-398): ss = x[0]^2 + x[1]^2 + ... as one running
-// fp32 sum in element order (one thread; v 16-byte aligned in LDS, n a multiple of 32).  The chain of adds is
-// the cost, so the LDS reads of the next 32 values are issued before the current 32 are added (the last batch
-// re-reads itself instead of branching), and the squares are formed off the chain.
-__device__ __forceinline__ float seq_sum_squares(const float *v, int n) {
-    const float4 *v4 = (const float4 *)v;
-    float ss = 0.0f;
-    float4 cur[8], nxt[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) cur[k] = v4[k];
-    for (int j = 0; j < n; j += 32) {
-        const int jn = min(j + 32, n - 32) / 4;
-#pragma unroll
-        for (int k = 0; k < 8; k++) nxt[k] = v4[jn + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            ss += cur[k].x * cur[k].x;
-            ss += cur[k].y * cur[k].y;
-            ss += cur[k].z * cur[k].z;
-            ss += cur[k].w * cur[k].w;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) cur[k] = nxt[k];
-    }
-    return ss;
-}
-
 // Sum of n floats in index order (one thread; p in LDS, any alignment): the reads of the next 16 values are
 // issued before the current 16 are added (the last batch re-reads itself instead of branching).
 __device__ __forceinline__ float seq_sum(const float *p, int n) {

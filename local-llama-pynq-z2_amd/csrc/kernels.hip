@@ -393,14 +393,13 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
             }
             KERNEL_MARK(2);
             float ss;
-            if (a.strict) { // one running sum in element order, as the reference's loop
+            if (a.strict) { // one running sum of the rounded squares in element order, as the reference's loop
 #pragma unroll
                 for (int k = 0; k < PRO_VEC; k++)
                     if (tid + k * nt < nv) sv4[tid + k * nt] = pn[k];
                 __syncthreads();
-                if (tid == 0) sred[0] = seq_sum_squares(sv, n);
-                __syncthreads();
-                ss = sred[0];
+                // its scratch: the gains' area when they stay in registers, else after them
+                ss = block_seq_sum<true>(sv, n, (uint8_t *)(sv + (nv <= PRO_VEC * nt ? n : 2 * n)));
             } else {
                 ss = block_sum(part, sred);
             }
@@ -665,7 +664,14 @@ size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
     size_t b = (size_t)ngp * W.gs + (size_t)ngp4 * 4 + (size_t)(threads / WAVE) * WAVE * 4 + (size_t)a.nb * W.rb * 4;
     if (a.ord) b += (size_t)a.nb * W.rb * (W.ng + 1) * 4; // group products of the ordered mode
     size_t extra = 0;
-    if (pro == PRO_NORM) extra = (size_t)W.n * 8;
+    if (pro == PRO_NORM) {
+        extra = (size_t)W.n * 8;
+        // the strict sum's scratch: where the gains would be parked when they stay in registers, else after them
+        if (a.strict) {
+            const size_t scr = seq_sum_scratch_bytes(threads);
+            extra = W.n / 4 <= PRO_VEC * threads ? std::max(extra, (size_t)W.n * 4 + scr) : extra + scr;
+        }
+    }
     if (pro == PRO_ATTN) extra = (size_t)W.n * 4 + (size_t)a.n_heads * a.att_splits * 4;
     if (epi == EPI_SWIGLU) extra = extra > (size_t)a.nb * W.rb * 2 ? extra : (size_t)a.nb * W.rb * 2;
     return b + extra + 16;

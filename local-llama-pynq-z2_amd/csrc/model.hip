@@ -462,7 +462,8 @@ struct Src { const uint8_t *w, *s; };
 int pick_shapes(llm_model *m) {
     const int cus = hip_cu_count(m->device);
     if (!cus) return -1;
-    const int ord = m->kind == 1 || m->strict;
+    // bit 0: ordered group sums; bit 1: the strict mode's sequential RMSNorm sum (it shapes the norm GEMVs)
+    const int ord = (m->kind == 1 || m->strict) | (m->strict ? 2 : 0);
     for (Layer &ly : m->L) {
         ly.s_qkv = gemv_pick_shape(ly.qkv, PRO_NORM, EPI_QKV, ord, cus);
         ly.s_o = gemv_pick_shape(ly.o, PRO_ATTN, EPI_RESID, ord, cus);

@@ -639,7 +639,7 @@ __global__ void __launch_bounds__(256) k_p_embed(ProwArgs a) {
 // 603-605), stored back, then normalized.
 template <bool RESID>
 __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
-    extern __shared__ __align__(16) float sv[]; // dim floats + 4 per wave
+    extern __shared__ __align__(16) float sv[]; // dim floats + 8, then the strict sum's scratch
     const int m = blockIdx.x, n = a.dim, nt = blockDim.x;
     float *x = a.x + (size_t)m * n;
     const float *y = a.y + (size_t)m * n;
@@ -678,11 +678,9 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
         part += v * v;
     }
     float ss;
-    if (a.strict) { // one running sum in element order (qwen.c:339, runq.c:396-398)
+    if (a.strict) { // one running sum of the rounded squares in element order (qwen.c:339, runq.c:396-398)
         __syncthreads();
-        if (threadIdx.x == 0) sv[n] = seq_sum_squares(sv, n);
-        __syncthreads();
-        ss = sv[n];
+        ss = block_seq_sum<true>(sv, n, (uint8_t *)(sv + n + 8));
     } else {
         ss = block_sum(part, sv + n);
     }
@@ -1201,8 +1199,10 @@ hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
 }
 hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st) {
     if (a.dim % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
-    if (resid) hipLaunchKernelGGL(k_p_norm_quant<true>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
-    else hipLaunchKernelGGL(k_p_norm_quant<false>, dim3(a.M), dim3(256), (size_t)(a.dim + 8) * 4, st, a);
+    // dim floats, 8 for the block sum, then the strict sequential sum's scratch
+    const size_t lds = (size_t)(a.dim + 8) * 4 + (a.strict ? seq_sum_scratch_bytes(256) : 0);
+    if (resid) hipLaunchKernelGGL(k_p_norm_quant<true>, dim3(a.M), dim3(256), lds, st, a);
+    else hipLaunchKernelGGL(k_p_norm_quant<false>, dim3(a.M), dim3(256), lds, st, a);
     return hipGetLastError();
 }
 hipError_t launch_p_qkv(const ProwArgs &a, hipStream_t st) {

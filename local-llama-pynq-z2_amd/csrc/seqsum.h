@@ -1,0 +1,112 @@
+// Sequential fp32 sums, bit for bit, by a whole block (gfx950, wave64).
+//
+// The reference adds the terms of a sum one after another in fp32 (rmsnorm's sum of squares, qwen.c:339 /
+// runq.c:396; the softmax denominator, qwen.c:349): s_k = fl(s_{k-1} + a_k).  One lane spends a dependent add
+// per term, 8.4 cycles on gfx950: 3.1 us for 896 terms, 12.6 us for 3584.
+//
+// Speculative segments.  The terms are cut into one segment per wave.  Before a segment the running sum is some
+// fp32 value s; the exact sum of the terms before the segment, rounded to fp32 (predicted as the fp64 sum of
+// the segments' fp32 totals), lies within a few ulps of s, because the reference's roundings drift from the exact sum by a random walk
+// (about sqrt(k/36) ulps after k terms of one sign).  Lane l of the segment's wave starts from the fp32 value
+// l - 32 ulps away from that prediction (its bit pattern +- l - 32) and adds the segment's terms in order, the
+// reference's own operation: all 64 candidate chains advance together, one add per term.  Wave 0 then walks
+// the segments: s after segment 0 is its exact chain (the lane that started from 0); s after segment k is the
+// end of the lane of segment k whose start equals s bit for bit, or, when s lies outside the 64 candidates,
+// segment k added again one term at a time from s.  Either way every step is the reference's fp32 add from the
+// reference's running value, so the result is the sequential sum exactly, for any terms (signs, inf, NaN).
+
+#pragma once
+#include "device.h"
+
+#define SEQ_MAX_WAVES 16 // segments (waves) a block may use
+
+// LDS the block function needs: every segment's 64 candidate ends, the segments' fp64 totals and predicted
+// start bits, and the result.
+__host__ __device__ inline size_t seq_sum_scratch_bytes(int threads) {
+    const int nw = threads / 64;
+    return (size_t)nw * 64 * 4 + (size_t)nw * 8 + (size_t)nw * 4 + 16;
+}
+
+// s_0 = 0, s_k = fl(s_{k-1} + t_k): the reference's sequential sum of the terms t_k = a[k-1], or with SQ the
+// rounded squares t_k = fl(a[k-1] * a[k-1]) (rmsnorm's loop, qwen.c:339).  a: LDS, 16-byte aligned, read by every
+// wave; scratch: seq_sum_scratch_bytes(blockDim.x) bytes of LDS, 16-byte aligned; at most SEQ_MAX_WAVES waves.
+// Every thread of the block calls it with the same n (barriers inside); every thread gets the result.
+template <bool SQ>
+__device__ __forceinline__ float seq_term(float v) {
+    if constexpr (SQ) return v * v;
+    return v;
+}
+template <bool SQ>
+__device__ __forceinline__ float block_seq_sum(const float *a, int n, uint8_t *scratch) {
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), nw = blockDim.x / WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
+    float *ends = (float *)scratch;                       // [nw][64]
+    double *tot = (double *)(ends + (size_t)nw * WAVE);   // [nw]
+    uint32_t *pbits = (uint32_t *)(tot + nw);             // [nw]
+    float *res = (float *)(pbits + nw);
+    // segments of L terms (a multiple of 4: every segment starts 16-byte aligned)
+    const int L = ((n + nw - 1) / nw + 3) & ~3;
+    const int q0 = min(wave * L, n), q1 = min(q0 + L, n);
+    // (1) each segment's total (fp32 by DPP: within a few ulps of the exact total), for the predictions
+    float t = 0.0f;
+    for (int i = q0 + lane; i < q1; i += WAVE) t += seq_term<SQ>(a[i]);
+    t = wave_sum(t);
+    if (lane == 0) tot[wave] = (double)t;
+    __syncthreads();
+    // (2) the candidate chains: lane l starts l - 32 ulps from the predicted start (segment 0: lane 32 from 0)
+    double pd = 0.0;
+    for (int k = 0; k < wave; k++) pd += tot[k];
+    const uint32_t pb = __float_as_uint((float)pd);
+    if (lane == 0) pbits[wave] = pb;
+    float s = __uint_as_float(pb + (uint32_t)lane - (uint32_t)(WAVE / 2));
+    const float4 *a4 = (const float4 *)a;
+    int i = q0;
+    if (i + 16 <= q1) {
+        // the terms as broadcast reads, the next 16 in flight while the current 16 are added
+        float4 cur[4], nxt[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) cur[r] = a4[i / 4 + r];
+        for (; i + 16 <= q1; i += 16) {
+            const int in = min(i + 16, q1 - 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) nxt[r] = a4[in / 4 + r];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s = s + seq_term<SQ>(cur[r].x);
+                s = s + seq_term<SQ>(cur[r].y);
+                s = s + seq_term<SQ>(cur[r].z);
+                s = s + seq_term<SQ>(cur[r].w);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) cur[r] = nxt[r];
+        }
+    }
+    for (; i < q1; i++) s = s + seq_term<SQ>(a[i]);
+    ends[(size_t)wave * WAVE + lane] = s;
+    __syncthreads();
+    // (3) the walk over the segments, on wave 0
+    if (wave == 0) {
+        float e[SEQ_MAX_WAVES];
+#pragma unroll
+        for (int k = 0; k < SEQ_MAX_WAVES; k++) e[k] = k < nw ? ends[(size_t)k * WAVE + lane] : 0.0f;
+        const uint32_t pl = lane < nw ? pbits[lane] : 0u;
+        uint32_t sb = __builtin_amdgcn_readlane(__float_as_uint(e[0]), WAVE / 2);
+#pragma unroll
+        for (int k = 1; k < SEQ_MAX_WAVES; k++) {
+            if (k < nw) {
+                const uint32_t idx = sb - __builtin_amdgcn_readlane(pl, k) + (uint32_t)(WAVE / 2);
+                if (idx < (uint32_t)WAVE) {
+                    sb = __builtin_amdgcn_readlane(__float_as_uint(e[k]), idx);
+                } else { // the running sum is not among the candidates: the segment again, term by term
+                    const int k0 = min(k * L, n), k1 = min(k0 + L, n);
+                    float x = __uint_as_float(sb);
+                    for (int j = k0; j < k1; j++) x = x + seq_term<SQ>(a[j]);
+                    sb = __builtin_amdgcn_readfirstlane(__float_as_uint(x));
+                }
+            }
+        }
+        if (lane == 0) *res = __uint_as_float(sb);
+    }
+    __syncthreads();
+    return *res;
+}
