@@ -179,7 +179,15 @@ __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc
     for (int w = 0; w < nw; w++) mx = fmaxf(mx, sred[w]);
     for (int t = tid; t < P; t += nt) sc[t] = ref_expf(sc[t] - mx);
     __syncthreads();
-    const float sum = block_seq_sum<false>(sc, P, sscr);
+    float sum;
+    if (P <= 256) { // a short sum: one lane, cheaper than the block's segments
+        if (tid == 0) sred[nw] = seq_sum(sc, P);
+        __syncthreads();
+        sum = sred[nw];
+    } else {
+        sum = block_seq_sum(sc, P, sscr);
+        __syncthreads(); // every wave's walk may still read the exponentials that the division below overwrites
+    }
     for (int t = tid; t < P; t += nt) sc[t] = sc[t] / sum;
     __syncthreads();
     for (int e = tid; e < hs; e += nt) {

@@ -394,12 +394,22 @@ __global__ void __launch_bounds__(D == 4 ? 512 : 1024) k_gemv(GemvArgs a) {
             KERNEL_MARK(2);
             float ss;
             if (a.strict) { // one running sum of the rounded squares in element order, as the reference's loop
+                // the squares x[i] * x[i] (each rounded, as the reference's), and after them the sum's scratch: in
+                // x's own area when x stays in registers, else after x and the gains parked in LDS
+                const bool regs = nv <= PRO_VEC * nt;
+                float4 *q4 = (float4 *)(regs ? sv : sv + 2 * n);
 #pragma unroll
                 for (int k = 0; k < PRO_VEC; k++)
-                    if (tid + k * nt < nv) sv4[tid + k * nt] = pn[k];
+                    if (tid + k * nt < nv) {
+                        const float4 v = pn[k];
+                        q4[tid + k * nt] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+                    }
+                for (int i = PRO_VEC * nt + tid; i < nv; i += nt) {
+                    const float4 v = sv4[i];
+                    q4[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+                }
                 __syncthreads();
-                // its scratch: the gains' area when they stay in registers, else after them
-                ss = block_seq_sum<true>(sv, n, (uint8_t *)(sv + (nv <= PRO_VEC * nt ? n : 2 * n)));
+                ss = block_seq_sum((const float *)q4, n, (uint8_t *)((float *)q4 + n));
             } else {
                 ss = block_sum(part, sred);
             }
@@ -666,10 +676,10 @@ size_t gemv_lds_bytes(const GemvArgs &a, int pro, int epi, int threads) {
     size_t extra = 0;
     if (pro == PRO_NORM) {
         extra = (size_t)W.n * 8;
-        // the strict sum's scratch: where the gains would be parked when they stay in registers, else after them
+        // the strict sum's squares and scratch: in x's area when x stays in registers, else after x and the gains
         if (a.strict) {
             const size_t scr = seq_sum_scratch_bytes(threads);
-            extra = W.n / 4 <= PRO_VEC * threads ? std::max(extra, (size_t)W.n * 4 + scr) : extra + scr;
+            extra = W.n / 4 <= PRO_VEC * threads ? std::max(extra, (size_t)W.n * 4 + scr) : (size_t)W.n * 12 + scr;
         }
     }
     if (pro == PRO_ATTN) extra = (size_t)W.n * 4 + (size_t)a.n_heads * a.att_splits * 4;

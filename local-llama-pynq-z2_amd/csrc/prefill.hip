@@ -639,7 +639,7 @@ __global__ void __launch_bounds__(256) k_p_embed(ProwArgs a) {
 // 603-605), stored back, then normalized.
 template <bool RESID>
 __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
-    extern __shared__ __align__(16) float sv[]; // dim floats + 8, then the strict sum's scratch
+    extern __shared__ __align__(16) float sv[]; // dim floats + 8, then the strict mode's squares and sum scratch
     const int m = blockIdx.x, n = a.dim, nt = blockDim.x;
     float *x = a.x + (size_t)m * n;
     const float *y = a.y + (size_t)m * n;
@@ -679,8 +679,11 @@ __global__ void __launch_bounds__(256) k_p_norm_quant(ProwArgs a) {
     }
     float ss;
     if (a.strict) { // one running sum of the rounded squares in element order (qwen.c:339, runq.c:396-398)
+        float *sq = sv + n + 8; // the squares (each rounded, as the reference's), then the sum's scratch
         __syncthreads();
-        ss = block_seq_sum<true>(sv, n, (uint8_t *)(sv + n + 8));
+        for (int i = threadIdx.x; i < n; i += nt) sq[i] = sv[i] * sv[i];
+        __syncthreads();
+        ss = block_seq_sum(sq, n, (uint8_t *)(sq + n));
     } else {
         ss = block_sum(part, sv + n);
     }
@@ -1199,8 +1202,8 @@ hipError_t launch_p_embed(const ProwArgs &a, hipStream_t st) {
 }
 hipError_t launch_p_norm_quant(const ProwArgs &a, bool resid, hipStream_t st) {
     if (a.dim % 4 || ((uintptr_t)a.oq & 3)) return hipErrorInvalidValue;
-    // dim floats, 8 for the block sum, then the strict sequential sum's scratch
-    const size_t lds = (size_t)(a.dim + 8) * 4 + (a.strict ? seq_sum_scratch_bytes(256) : 0);
+    // dim floats, 8 for the block sum, then the strict mode's squares and sequential sum's scratch
+    const size_t lds = (size_t)(a.dim + 8) * 4 + (a.strict ? (size_t)a.dim * 4 + seq_sum_scratch_bytes(256) : 0);
     if (resid) hipLaunchKernelGGL(k_p_norm_quant<true>, dim3(a.M), dim3(256), lds, st, a);
     else hipLaunchKernelGGL(k_p_norm_quant<false>, dim3(a.M), dim3(256), lds, st, a);
     return hipGetLastError();

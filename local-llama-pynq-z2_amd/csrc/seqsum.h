@@ -12,7 +12,7 @@
 // reference's own operation: all 64 candidate chains advance together, one add per term.  Wave 0 then walks
 // the segments: s after segment 0 is its exact chain (the lane that started from 0); s after segment k is the
 // end of the lane of segment k whose start equals s bit for bit, or, when s lies outside the 64 candidates,
-// segment k added again one term at a time from s.  Either way every step is the reference's fp32 add from the
+// segment k added again one term at a time from s (every wave walks, so no barrier follows).  Either way every step is the reference's fp32 add from the
 // reference's running value, so the result is the sequential sum exactly, for any terms (signs, inf, NaN).
 
 #pragma once
@@ -21,41 +21,52 @@
 #define SEQ_MAX_WAVES 16 // segments (waves) a block may use
 
 // LDS the block function needs: every segment's 64 candidate ends, the segments' fp64 totals and predicted
-// start bits, and the result.
+// start bits.
 __host__ __device__ inline size_t seq_sum_scratch_bytes(int threads) {
     const int nw = threads / 64;
     return (size_t)nw * 64 * 4 + (size_t)nw * 8 + (size_t)nw * 4 + 16;
 }
 
-// s_0 = 0, s_k = fl(s_{k-1} + t_k): the reference's sequential sum of the terms t_k = a[k-1], or with SQ the
-// rounded squares t_k = fl(a[k-1] * a[k-1]) (rmsnorm's loop, qwen.c:339).  a: LDS, 16-byte aligned, read by every
-// wave; scratch: seq_sum_scratch_bytes(blockDim.x) bytes of LDS, 16-byte aligned; at most SEQ_MAX_WAVES waves.
-// Every thread of the block calls it with the same n (barriers inside); every thread gets the result.
-template <bool SQ>
-__device__ __forceinline__ float seq_term(float v) {
-    if constexpr (SQ) return v * v;
+// Inclusive prefix sum of a double over each row of 16 lanes (DPP row shifts on both halves).
+__device__ __forceinline__ double row_incl_scan_f64(double v) {
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) {
+        const int lo = __double2loint(v), hi = __double2hiint(v);
+        int l2, h2;
+        switch (sh) { // DPP controls are immediates
+        case 1: l2 = __builtin_amdgcn_update_dpp(0, lo, 0x111, 0xf, 0xf, true); h2 = __builtin_amdgcn_update_dpp(0, hi, 0x111, 0xf, 0xf, true); break;
+        case 2: l2 = __builtin_amdgcn_update_dpp(0, lo, 0x112, 0xf, 0xf, true); h2 = __builtin_amdgcn_update_dpp(0, hi, 0x112, 0xf, 0xf, true); break;
+        case 4: l2 = __builtin_amdgcn_update_dpp(0, lo, 0x114, 0xf, 0xf, true); h2 = __builtin_amdgcn_update_dpp(0, hi, 0x114, 0xf, 0xf, true); break;
+        default: l2 = __builtin_amdgcn_update_dpp(0, lo, 0x118, 0xf, 0xf, true); h2 = __builtin_amdgcn_update_dpp(0, hi, 0x118, 0xf, 0xf, true); break;
+        }
+        v += __hiloint2double(h2, l2);
+    }
     return v;
 }
-template <bool SQ>
+
+// s_0 = 0, s_k = fl(s_{k-1} + a[k-1]): the reference's sequential sum of a[0 .. n).  a: LDS, 16-byte aligned, read
+// by every wave; scratch: seq_sum_scratch_bytes(blockDim.x) bytes of LDS, 16-byte aligned; at most SEQ_MAX_WAVES
+// waves.  Every thread of the block calls it with the same n (barriers inside); every thread gets the result.
 __device__ __forceinline__ float block_seq_sum(const float *a, int n, uint8_t *scratch) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), nw = blockDim.x / WAVE;
     const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
     float *ends = (float *)scratch;                       // [nw][64]
     double *tot = (double *)(ends + (size_t)nw * WAVE);   // [nw]
     uint32_t *pbits = (uint32_t *)(tot + nw);             // [nw]
-    float *res = (float *)(pbits + nw);
     // segments of L terms (a multiple of 4: every segment starts 16-byte aligned)
     const int L = ((n + nw - 1) / nw + 3) & ~3;
     const int q0 = min(wave * L, n), q1 = min(q0 + L, n);
     // (1) each segment's total (fp32 by DPP: within a few ulps of the exact total), for the predictions
     float t = 0.0f;
-    for (int i = q0 + lane; i < q1; i += WAVE) t += seq_term<SQ>(a[i]);
+    for (int i = q0 + lane; i < q1; i += WAVE) t += a[i];
     t = wave_sum(t);
     if (lane == 0) tot[wave] = (double)t;
     __syncthreads();
-    // (2) the candidate chains: lane l starts l - 32 ulps from the predicted start (segment 0: lane 32 from 0)
-    double pd = 0.0;
-    for (int k = 0; k < wave; k++) pd += tot[k];
+    // (2) the candidate chains: lane l starts l - 32 ulps from the predicted start (segment 0: lane 32 from 0);
+    // the prediction is the fp64 sum of the totals before the segment (a row scan of the <= 16 totals)
+    const double pref = row_incl_scan_f64(lane < nw ? tot[min(lane, SEQ_MAX_WAVES - 1)] : 0.0);
+    const double pd = wave == 0 ? 0.0 : __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(pref), wave - 1),
+                                                          __builtin_amdgcn_readlane(__double2loint(pref), wave - 1));
     const uint32_t pb = __float_as_uint((float)pd);
     if (lane == 0) pbits[wave] = pb;
     float s = __uint_as_float(pb + (uint32_t)lane - (uint32_t)(WAVE / 2));
@@ -72,41 +83,46 @@ __device__ __forceinline__ float block_seq_sum(const float *a, int n, uint8_t *s
             for (int r = 0; r < 4; r++) nxt[r] = a4[in / 4 + r];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                s = s + seq_term<SQ>(cur[r].x);
-                s = s + seq_term<SQ>(cur[r].y);
-                s = s + seq_term<SQ>(cur[r].z);
-                s = s + seq_term<SQ>(cur[r].w);
+                s = s + cur[r].x;
+                s = s + cur[r].y;
+                s = s + cur[r].z;
+                s = s + cur[r].w;
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) cur[r] = nxt[r];
         }
     }
-    for (; i < q1; i++) s = s + seq_term<SQ>(a[i]);
+    for (; i < q1; i++) s = s + a[i];
     ends[(size_t)wave * WAVE + lane] = s;
     __syncthreads();
-    // (3) the walk over the segments, on wave 0
-    if (wave == 0) {
-        float e[SEQ_MAX_WAVES];
+    // (3) the walk over the segments, by every wave (no barrier after it): each step takes the end of the lane
+    // whose start is the running sum; a step outside the candidates sends the walk to the term-by-term path
+    float e[SEQ_MAX_WAVES];
 #pragma unroll
-        for (int k = 0; k < SEQ_MAX_WAVES; k++) e[k] = k < nw ? ends[(size_t)k * WAVE + lane] : 0.0f;
-        const uint32_t pl = lane < nw ? pbits[lane] : 0u;
-        uint32_t sb = __builtin_amdgcn_readlane(__float_as_uint(e[0]), WAVE / 2);
+    for (int k = 0; k < SEQ_MAX_WAVES; k++) e[k] = k < nw ? ends[(size_t)k * WAVE + lane] : 0.0f;
+    const uint32_t pl = lane < nw ? pbits[min(lane, SEQ_MAX_WAVES - 1)] : 0u;
+    uint32_t sb = __builtin_amdgcn_readlane(__float_as_uint(e[0]), WAVE / 2), miss = 0;
 #pragma unroll
-        for (int k = 1; k < SEQ_MAX_WAVES; k++) {
-            if (k < nw) {
-                const uint32_t idx = sb - __builtin_amdgcn_readlane(pl, k) + (uint32_t)(WAVE / 2);
-                if (idx < (uint32_t)WAVE) {
-                    sb = __builtin_amdgcn_readlane(__float_as_uint(e[k]), idx);
-                } else { // the running sum is not among the candidates: the segment again, term by term
-                    const int k0 = min(k * L, n), k1 = min(k0 + L, n);
-                    float x = __uint_as_float(sb);
-                    for (int j = k0; j < k1; j++) x = x + seq_term<SQ>(a[j]);
-                    sb = __builtin_amdgcn_readfirstlane(__float_as_uint(x));
-                }
+    for (int k = 1; k < SEQ_MAX_WAVES; k++) {
+        if (k < nw) {
+            const uint32_t idx = sb - __builtin_amdgcn_readlane(pl, k) + (uint32_t)(WAVE / 2);
+            miss |= idx >= (uint32_t)WAVE;
+            sb = __builtin_amdgcn_readlane(__float_as_uint(e[k]), idx & (WAVE - 1));
+        }
+    }
+    if (miss) { // again with the term-by-term path for the segments whose start is not among the candidates
+        sb = __builtin_amdgcn_readlane(__float_as_uint(e[0]), WAVE / 2);
+        for (int k = 1; k < nw; k++) {
+            const uint32_t idx = sb - __builtin_amdgcn_readlane(pl, k) + (uint32_t)(WAVE / 2);
+            if (idx < (uint32_t)WAVE) {
+                sb = __builtin_amdgcn_readlane(__float_as_uint(ends[(size_t)k * WAVE + lane]), idx);
+            } else {
+                const int k0 = min(k * L, n), k1 = min(k0 + L, n);
+                float x = __uint_as_float(sb);
+                for (int j = k0; j < k1; j++) x = x + a[j];
+                sb = __builtin_amdgcn_readfirstlane(__float_as_uint(x));
             }
         }
-        if (lane == 0) *res = __uint_as_float(sb);
     }
-    __syncthreads();
-    return *res;
+    return __uint_as_float(sb);
 }
