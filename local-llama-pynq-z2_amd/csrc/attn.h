@@ -142,69 +142,169 @@ __device__ __forceinline__ void attn_range(const float *q, const float *kc, cons
 //   score_t = (sum over i in order of q[i] * k_t[i]) / sqrtf(hs);  max over t (exact in any order);
 //   e_t = expf(score_t - max) (ref_expf: the reference libm's expf);  sum = e_0 + e_1 + ... in position order;
 //   a_t = e_t / sum;  out[e] = ((0 + a_0 v_0[e]) + a_1 v_1[e]) + ... in position order.
-// The scores and products run in parallel; the two running sums are single chains, as in the reference.
+// The scores (a position per thread) and the products run in parallel, V staged in LDS tiles whose loads run
+// ahead; the running sums are the reference's chains (the softmax sum by the block's speculative segments when
+// long).  Block of 256 threads, hs <= 256.
 // Block-wide (barriers inside); every thread of the block calls it.  sm: attn_strict_lds_floats floats.
 
+// Positions of V one tile stages in LDS (8192 floats at most: 8 16-byte loads per thread of 256).
+__host__ __device__ inline int attn_strict_tile(int hs) { return 8192 / hs < 256 ? 8192 / hs : 256; }
 __host__ __device__ inline size_t attn_strict_lds_floats(int hs, int P, int threads) {
     return (size_t)hs + (((size_t)P + 3) & ~(size_t)3) + (((size_t)threads / WAVE + 4 + 3) & ~(size_t)3) +
-           seq_sum_scratch_bytes(threads) / 4 + 4;
+           seq_sum_scratch_bytes(threads) / 4 + 4 + (size_t)attn_strict_tile(hs) * hs;
 }
 
+// HS: the head size as a compile-time constant (64, 128: a full tile's chain is straight-line code, so the
+// next tile's loads stay in flight under it), or 0 for any other hs.
+template <int HS>
 __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc, const float *vc, int kv_dim,
-                                                 int koff, int hs, int P, float *sm, float *out) {
+                                                 int koff, int hs_arg, int P, float *sm, float *out) {
+    const int hs = HS ? HS : hs_arg;
     const int tid = threadIdx.x, nt = blockDim.x, lane = tid & (WAVE - 1), wave = tid / WAVE, nw = nt / WAVE;
     float *sq = sm, *sc = sm + hs, *sred = sc + ((P + 3) & ~3);
     uint8_t *sscr = (uint8_t *)(sred + ((nw + 4 + 3) & ~3)); // the sequential sum's scratch (16-byte aligned)
+    float *svt = (float *)(sscr + seq_sum_scratch_bytes(nt) + 16); // a tile of V rows [CH][hs]
+    const int CH = attn_strict_tile(hs), hs4 = hs / 4, ntile = (P + CH - 1) / CH;
+    // V tiles: 8 16-byte loads per thread (vector j * 256 + tid of the tile: position / hs4, column % hs4), rows
+    // past P read nothing; the first tile's loads leave now, behind the scores
+    const auto rv = __builtin_amdgcn_make_buffer_rsrc((void *)(vc + koff), 0, (int)(((size_t)(P - 1) * kv_dim + hs) * 4),
+                                                      0x00020000);
+    auto vtile_load = [&](int k, f32x4 (&r)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int idx = j * 256 + tid, t = k * CH + idx / hs4, c = idx - (idx / hs4) * hs4;
+            const bool ok = idx < CH * hs4 && t < P;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rv, ok ? (uint32_t)(t * kv_dim + 4 * c) * 4u : 0x80000000u, 0, 0);
+            r[j] = *(const f32x4 *)&v;
+        }
+    };
+    auto vtile_store = [&](const f32x4 (&r)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int idx = j * 256 + tid;
+            if (idx < CH * hs4) ((f32x4 *)svt)[idx] = r[j];
+        }
+    };
+    f32x4 vr[8];
+    vtile_load(0, vr);
+    KERNEL_MARK(0);
     for (int i = tid; i < hs; i += nt) sq[i] = q[i];
     __syncthreads();
+    KERNEL_MARK(1);
     const float rs = sqrtf((float)hs);
-    float mx = -INFINITY;
-    for (int t = tid; t < P; t += nt) {
-        const f32x4 *k4 = (const f32x4 *)(kc + (size_t)t * kv_dim + koff);
-        float d = 0.0f;
-        for (int i4 = 0; i4 < hs / 4; i4++) {
-            const f32x4 kk = k4[i4];
-            d += sq[4 * i4] * kk.x;
-            d += sq[4 * i4 + 1] * kk.y;
-            d += sq[4 * i4 + 2] * kk.z;
-            d += sq[4 * i4 + 3] * kk.w;
+    const f32x4 *q4 = (const f32x4 *)sq;
+    // scores: a position per thread, its K row through a buffer resource (the row's offset per lane, the
+    // column's as a scalar), 4 vectors a batch, two batches in flight (ping-pong: each waits for its own loads)
+    const auto rk = __builtin_amdgcn_make_buffer_rsrc((void *)(kc + koff), 0, (int)(((size_t)(P - 1) * kv_dim + hs) * 4),
+                                                      0x00020000);
+    auto kbatch = [&](uint32_t vo, int c, f32x4 (&b)[4]) { // vectors c .. c+3 of the row (past hs4: zeros)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rk, c + j < hs4 ? vo : 0x80000000u, (c + j) * 16, 0);
+            b[j] = *(const f32x4 *)&v;
         }
-        const float s = d / rs;
-        sc[t] = s;
-        mx = fmaxf(mx, s);
+    };
+    auto kuse = [&](float d, int c, const f32x4 (&b)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f32x4 kk = b[j], qq = q4[c + j];
+            d += qq.x * kk.x;
+            d += qq.y * kk.y;
+            d += qq.z * kk.z;
+            d += qq.w * kk.w;
+        }
+        return d;
+    };
+    float mx = -INFINITY;
+    for (int t0 = 0; t0 < P; t0 += nt) {
+        const int t = t0 + tid;
+        const uint32_t vo = (uint32_t)min(t, P - 1) * (uint32_t)kv_dim * 4u;
+        float d = 0.0f;
+        if ((hs4 & 7) == 0) { // whole batches: no guards inside the chain
+            f32x4 bA[4], bB[4];
+            kbatch(vo, 0, bA);
+            for (int c = 0; c < hs4; c += 8) {
+                kbatch(vo, c + 4, bB);
+                d = kuse(d, c, bA);
+                kbatch(vo, c + 8, bA);
+                d = kuse(d, c + 4, bB);
+            }
+        } else {
+            const f32x4 *k4 = (const f32x4 *)(kc + (size_t)min(t, P - 1) * kv_dim + koff);
+            for (int c = 0; c < hs4; c++) {
+                const f32x4 kk = k4[c], qq = q4[c];
+                d += qq.x * kk.x;
+                d += qq.y * kk.y;
+                d += qq.z * kk.z;
+                d += qq.w * kk.w;
+            }
+        }
+        if (t < P) {
+            const float sct = d / rs;
+            sc[t] = sct;
+            mx = fmaxf(mx, sct);
+        }
     }
+    KERNEL_MARK(2);
     mx = wave_max(mx);
     if (lane == 0) sred[wave] = mx;
     __syncthreads();
     for (int w = 0; w < nw; w++) mx = fmaxf(mx, sred[w]);
     for (int t = tid; t < P; t += nt) sc[t] = ref_expf(sc[t] - mx);
     __syncthreads();
+    KERNEL_MARK(3);
     float sum;
-    if (P <= 256) { // a short sum: one lane, cheaper than the block's segments
-        if (tid == 0) sred[nw] = seq_sum(sc, P);
+    if (P <= 256) { // a short sum: one chain (wave 0, broadcast reads), cheaper than the block's segments
+        if (wave == 0) {
+            const float v = wave_seq_sum(sc, P);
+            if (lane == 0) sred[nw] = v;
+        }
         __syncthreads();
         sum = sred[nw];
     } else {
         sum = block_seq_sum(sc, P, sscr);
         __syncthreads(); // every wave's walk may still read the exponentials that the division below overwrites
     }
+    KERNEL_MARK(4);
     for (int t = tid; t < P; t += nt) sc[t] = sc[t] / sum;
     __syncthreads();
-    for (int e = tid; e < hs; e += nt) {
-        const float *v = vc + koff + e;
-        float acc = 0.0f;
-        int t = 0;
-        for (; t + 8 <= P; t += 8) {
-            float vv[8], aa[8];
+    KERNEL_MARK(5);
+    // values: an element per thread in the reference's position order, from the V tile in LDS; the next tile's
+    // loads are in flight while this one is summed
+    float acc = 0.0f;
+    const int e = tid < hs ? tid : 0;
+    for (int k = 0; k < ntile; k++) {
+        vtile_store(vr);
+        __syncthreads();
+        if (k + 1 < ntile) vtile_load(k + 1, vr);
+        const int t0 = k * CH, T = min(CH, P - t0);
+        if (tid < hs) {
+            const float *vt = svt + e;
+            const f32x4 *w4 = (const f32x4 *)(sc + t0);
+            if (HS && T == CH) { // a full tile: straight-line code
+                constexpr int CHC = HS ? (8192 / HS < 256 ? 8192 / HS : 256) : 4;
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
-                vv[u] = v[(size_t)(t + u) * kv_dim];
-                aa[u] = sc[t + u];
+                for (int t = 0; t < CHC; t += 4) {
+                    const f32x4 w = w4[t / 4];
+                    acc += w.x * vt[t * HS];
+                    acc += w.y * vt[(t + 1) * HS];
+                    acc += w.z * vt[(t + 2) * HS];
+                    acc += w.w * vt[(t + 3) * HS];
+                }
+            } else {
+                int t = 0;
+                for (; t + 4 <= T; t += 4) {
+                    const f32x4 w = w4[t / 4];
+                    acc += w.x * vt[t * hs];
+                    acc += w.y * vt[(t + 1) * hs];
+                    acc += w.z * vt[(t + 2) * hs];
+                    acc += w.w * vt[(t + 3) * hs];
+                }
+                for (; t < T; t++) acc += sc[t0 + t] * vt[t * hs];
             }
-#pragma unroll
-            for (int u = 0; u < 8; u++) acc += aa[u] * vv[u];
         }
-        for (; t < P; t++) acc += sc[t] * v[(size_t)t * kv_dim];
-        out[e] = acc;
+        __syncthreads(); // the next tile's stores overwrite this one
     }
+    if (tid < hs) out[tid] = acc;
+    KERNEL_MARK(6);
 }

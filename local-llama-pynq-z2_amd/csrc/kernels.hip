@@ -911,11 +911,12 @@ __global__ void __launch_bounds__(512) k_attention_short(AttnArgs a) {
 
 // Reference-order decode attention: block h is query head h over positions 0 .. pos (attn_strict_head); the
 // output goes to acc[h][0..hs) with (max, sum) = (0, 1), one slice whose merge is the identity.
+template <int HS>
 __global__ void __launch_bounds__(256) k_attention_strict(AttnArgs a) {
     extern __shared__ __align__(16) float sm[];
     const int pos = a.ctrl->pos, h = blockIdx.x, kv_mul = a.n_heads / a.n_kv, hs = a.hs;
-    attn_strict_head(a.q + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs, pos + 1, sm,
-                     a.acc + (size_t)h * hs);
+    attn_strict_head<HS>(a.q + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs, pos + 1, sm,
+                         a.acc + (size_t)h * hs);
     if (threadIdx.x == 0) {
         a.ml[2 * h] = 0.0f;
         a.ml[2 * h + 1] = 1.0f;
@@ -924,9 +925,14 @@ __global__ void __launch_bounds__(256) k_attention_strict(AttnArgs a) {
 
 hipError_t launch_attention_strict(const AttnArgs &a, hipStream_t st) {
     const size_t lds = attn_strict_lds_floats(a.hs, a.max_pos, 256) * 4;
-    if (a.hs % 4 || ((uintptr_t)a.kc & 15) || (a.kv_dim % 4) || a.max_pos < 1 || lds > 65536 || a.n_heads % a.n_kv)
+    // the K and V reads go through buffer resources: a layer's cache must stay below 2 GiB
+    if (a.hs % 4 || a.hs > 256 || ((uintptr_t)a.kc & 15) || (a.kv_dim % 4) || a.max_pos < 1 || lds > 65536 ||
+        a.n_heads % a.n_kv ||
+        (size_t)(a.max_pos + 64) * a.kv_dim * 4 >= 0x7fffffffu)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attention_strict, dim3(a.n_heads), dim3(256), lds, st, a);
+    if (a.hs == 64) hipLaunchKernelGGL(k_attention_strict<64>, dim3(a.n_heads), dim3(256), lds, st, a);
+    else if (a.hs == 128) hipLaunchKernelGGL(k_attention_strict<128>, dim3(a.n_heads), dim3(256), lds, st, a);
+    else hipLaunchKernelGGL(k_attention_strict<0>, dim3(a.n_heads), dim3(256), lds, st, a);
     return hipGetLastError();
 }
 

@@ -1180,10 +1180,11 @@ __global__ void __launch_bounds__(256) k_p_attn_merge(ProwArgs a, int all) {
 
 // Reference-order causal attention: block (h, m) is query head h of token m over positions 0 .. p0 + m
 // (attn_strict_head); the fp32 output row goes to xb[m], quantized afterwards by k_p_quant_rows.
+template <int HS>
 __global__ void __launch_bounds__(256) k_p_attn_strict(ProwArgs a) {
     extern __shared__ __align__(16) float sm[];
     const int h = blockIdx.x, m = blockIdx.y, hs = a.head_size, kv_mul = a.n_heads / a.n_kv;
-    attn_strict_head(a.q + (size_t)m * a.dim + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs,
+    attn_strict_head<HS>(a.q + (size_t)m * a.dim + (size_t)h * hs, a.kc, a.vc, a.kv_dim, (h / kv_mul) * hs, hs,
                      a.p0 + m + 1, sm, a.xb + (size_t)m * a.dim + (size_t)h * hs);
 }
 
@@ -1227,10 +1228,14 @@ hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
     const int kv_mul = a.n_heads / a.n_kv, hs = a.head_size;
     if (a.strict) {
         const size_t lds = attn_strict_lds_floats(hs, a.p0 + a.M, 256) * 4;
-        if (hs % 4 || ((uintptr_t)a.kc & 15) || a.kv_dim % 4 || a.dim % 4 || a.dim % a.gs || !a.xb ||
-            ((uintptr_t)a.oq & 3) || lds > 65536 || a.n_heads % a.n_kv)
+        // (the K and V reads go through buffer resources: a layer's cache stays below 2 GiB)
+        if (hs % 4 || hs > 256 || ((uintptr_t)a.kc & 15) || a.kv_dim % 4 || a.dim % 4 || a.dim % a.gs || !a.xb ||
+            ((uintptr_t)a.oq & 3) || lds > 65536 || a.n_heads % a.n_kv ||
+            (size_t)(a.p0 + a.M + 64) * a.kv_dim * 4 >= 0x7fffffffu)
             return hipErrorInvalidValue;
-        hipLaunchKernelGGL(k_p_attn_strict, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
+        if (hs == 64) hipLaunchKernelGGL(k_p_attn_strict<64>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
+        else if (hs == 128) hipLaunchKernelGGL(k_p_attn_strict<128>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
+        else hipLaunchKernelGGL(k_p_attn_strict<0>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(k_p_quant_rows, dim3(a.M), dim3(256), (size_t)a.dim * 4, st, a);

@@ -27,6 +27,35 @@ __host__ __device__ inline size_t seq_sum_scratch_bytes(int threads) {
     return (size_t)nw * 64 * 4 + (size_t)nw * 8 + (size_t)nw * 4 + 16;
 }
 
+// s_0 = 0, s_k = fl(s_{k-1} + a[k-1]) as one chain by the whole wave (every lane the same values; a: LDS, 16-byte
+// aligned): the terms as broadcast reads, the next 16 in flight while the current 16 are added.
+__device__ __forceinline__ float wave_seq_sum(const float *a, int n) {
+    const float4 *a4 = (const float4 *)a;
+    float s = 0.0f;
+    int i = 0;
+    if (n >= 16) {
+        float4 cur[4], nxt[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) cur[r] = a4[r];
+        for (; i + 16 <= n; i += 16) {
+            const int in = min(i + 16, n - 16) & ~3;
+#pragma unroll
+            for (int r = 0; r < 4; r++) nxt[r] = a4[in / 4 + r];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                s = s + cur[r].x;
+                s = s + cur[r].y;
+                s = s + cur[r].z;
+                s = s + cur[r].w;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) cur[r] = nxt[r];
+        }
+    }
+    for (; i < n; i++) s = s + a[i];
+    return s;
+}
+
 // Inclusive prefix sum of a double over each row of 16 lanes (DPP row shifts on both halves).
 __device__ __forceinline__ double row_incl_scan_f64(double v) {
 #pragma unroll
