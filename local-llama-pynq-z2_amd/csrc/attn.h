@@ -220,7 +220,22 @@ __device__ __forceinline__ void attn_strict_head(const float *q, const float *kc
         const int t = t0 + tid;
         const uint32_t vo = (uint32_t)min(t, P - 1) * (uint32_t)kv_dim * 4u;
         float d = 0.0f;
-        if ((hs4 & 7) == 0) { // whole batches: no guards inside the chain
+        if constexpr (HS != 0) { // the whole row in flight at once
+            f32x4 kr[HS / 4];
+#pragma unroll
+            for (int j = 0; j < HS / 4; j++) {
+                const auto v = __builtin_amdgcn_raw_buffer_load_b128(rk, vo, j * 16, 0);
+                kr[j] = *(const f32x4 *)&v;
+            }
+#pragma unroll
+            for (int j = 0; j < HS / 4; j++) {
+                const f32x4 kk = kr[j], qq = q4[j];
+                d += qq.x * kk.x;
+                d += qq.y * kk.y;
+                d += qq.z * kk.z;
+                d += qq.w * kk.w;
+            }
+        } else if ((hs4 & 7) == 0) { // whole batches: no guards inside the chain
             f32x4 bA[4], bB[4];
             kbatch(vo, 0, bA);
             for (int c = 0; c < hs4; c += 8) {
