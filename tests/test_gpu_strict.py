@@ -11,7 +11,7 @@ restated on the checking side.  The workloads:
   C2  llama2.c 768/12L .bin, 8-token prompt, greedy to the full 1024 positions (the KV cache fills)
   C3  Qwen2 0.5B-shape .qwb (24 layers, 65536-row head), 24-token prompt, 128 greedy tokens
   C4  the C3 model, 512-token batched prefill, then 64 greedy tokens
-  C5  Qwen2 7B-shape .qwb (28 layers, 152064-row head), context 4096, 32-token prompt, 32 greedy tokens
+  C5  Qwen2 7B-shape .qwb (28 layers, 152064-row head), context 4096, 32-token prompt, 256 greedy tokens
 Seeds of the synthetic models and prompts are fixed below."""
 import ctypes as C
 import os
@@ -244,17 +244,21 @@ def test_strict_c4_prefill_512_then_64_tokens(c3_model):
     m.close()
 
 
-def test_strict_c5_full_depth_context_4096(tmp_path):
+def test_strict_c5_full_workload_256_tokens_context_4096(tmp_path):
+    """the whole C5 workload: a 32-token prompt and 256 greedy tokens with a 4096-position cache (positions up
+    to 287), every logit, id and K/V row bit for bit"""
+    import time
     p = synth("qwb", str(tmp_path / "c5.qwb"), "c5", 35)
     ctx = 4096
     ref = RefQwen(p, ctx)
     prompt = c3_prompt(ref.head_ids, 32, 36)
-    ids_r, lg_r = ref.generate(prompt, 32)
-    print(f"C5 reference: {len(ids_r)} ids over {len(lg_r)} positions")
-    assert len(lg_r) >= 32 + 8  # a stop id (in the untrimmed head) may end the stream early, at both sides
+    t = time.time()
+    ids_r, lg_r = ref.generate(prompt, 256)
+    print(f"C5 reference: {len(ids_r)} ids over {len(lg_r)} positions in {time.time() - t:.1f} s", flush=True)
+    assert len(lg_r) >= 32 + 64  # a stop id (in the untrimmed head) may end the stream early, at both sides
     m = pkg().Model(p, ctx)
     m.set_strict(True)
-    r = m.generate(prompt, 32, logits=True)
+    r = m.generate(prompt, 256, logits=True)
     check_bitwise(m, ref, r["ids"], r["logits"], ids_r, lg_r, len(lg_r))
     m.close()
 
