@@ -21,6 +21,8 @@ the fast mode (tree sums) is timed too and reported as the sub-record "fast".  -
   copy of 1 GiB, then the prompt and 4 decode steps as eager launches, in the timed mode), or from earlier passes:
     python bench.py --traffic-from D ...      (D/fetch, D/write: rocprofv3 -d directories of the two passes)
   (c4: the 512-token prompt as one batched int8-MFMA prefill, timed over --steps repetitions, in both modes)
+  The c3 run also reports "dropin": the reference's own qwen.c host built with -DFPGA against libmatvec_hip.so
+  over the same workload (its tok/s and its FPGA_CHECK max abs diff, default and LLM_STRICT=1).
 
 Also reported: per-kernel roofline (each kernel kind's device time inside the replayed step graph, from HIP
 events around graph replays with and without that kind's launches, and its algorithmic bytes per launch);
@@ -164,6 +166,60 @@ def reference_run(cfg, path, prompt, n_new, n_logits):
         return None
     ids = [int(v) for v in r.stdout.strip().split(",") if v]
     return ids, np.fromfile(dump, np.float32).reshape(-1, n_logits)
+
+
+def dropin_record(cfg, path, prompt, n_new, ref, n_logits):
+    """the reference's own qwen.c host built unmodified with -DFPGA against libmatvec_hip.so (oracle/_ref/qwen-hip:
+    every matmul() through fpga_matvec4, the rest of forward() and the sampler on the host cores) over the
+    workload: its decode rate in qwen.c's definition, and its FPGA_CHECK line (every matmul also on the CPU,
+    qwen.c:103-112) over 8 greedy tokens in the default mode and with LLM_STRICT=1 (groups added in the
+    reference's order: the logits of every position then bitwise those of the strict CPU build)"""
+    exe = os.path.join(REPO, "oracle", "_ref", "qwen-hip")
+    if cfg["ref"] != "qwen" or not os.path.exists(exe):
+        return None
+    base = ref_args(cfg, path, prompt, n_new)
+
+    def run(n, **env):
+        args = base[:]
+        args[args.index("-n") + 1] = str(n)
+        dump = os.path.join(os.environ.get("BENCH_MODEL_DIR", "/tmp/llm_hip_bench"), "dropin.logits")
+        r = subprocess.run([exe] + args + ["--logits", dump], capture_output=True, text=True, timeout=900,
+                           env=dict(os.environ, OMP_NUM_THREADS=str(omp_threads()), **env))
+        if r.returncode != 0:
+            log(f"drop-in run failed: {r.stderr[-400:]}")
+            return None
+        rate = re.search(r"generated: (\d+) tokens, ([0-9.]+) tok/s", r.stderr)
+        chk = re.search(r"FPGA_CHECK: (\d+) matmuls, max abs diff ([-0-9.e+na]+), max rel diff ([-0-9.e+na]+)",
+                        r.stderr)
+        ids = [int(v) for v in r.stdout.strip().split(",") if v]
+        return {"ids": ids, "rate": float(rate.group(2)) if rate else None, "tokens": int(rate.group(1)) if rate else 0,
+                "check": (int(chk.group(1)), float(chk.group(2)), float(chk.group(3))) if chk else None,
+                "logits": np.fromfile(dump, np.float32).reshape(-1, n_logits)}
+
+    timed = run(n_new)
+    timed_strict = run(n_new, LLM_STRICT="1")
+    fast = run(8, FPGA_CHECK="1")
+    strict = run(8, FPGA_CHECK="1", LLM_STRICT="1")
+    if not (timed and timed_strict and fast and strict):
+        return None
+    rec = {"value": timed["rate"], "unit": "tok/s", "tokens": timed["tokens"],
+           "host": f"qwen.c -DFPGA (unmodified, strict IEEE build, OpenMP {omp_threads()} threads) + libmatvec_hip.so",
+           "ids_equal_reference": bool(ref) and timed["ids"] == ref[0][:len(timed["ids"])],
+           "fpga_check": {"matmuls": fast["check"][0], "max_abs_diff": fast["check"][1],
+                          "max_rel_diff": fast["check"][2], "tokens": 8} if fast["check"] else None,
+           "strict": {"value": timed_strict["rate"], "unit": "tok/s",
+                      "ids_equal_reference": bool(ref) and timed_strict["ids"] == ref[0][:len(timed_strict["ids"])],
+                      "fpga_check_matmuls": strict["check"][0] if strict["check"] else None,
+                      "fpga_check_max_abs_diff": strict["check"][1] if strict["check"] else None,
+                      "positions": int(len(strict["logits"])),
+                      "bitwise_identical_logits": bool(ref) and len(ref[1]) >= len(strict["logits"]) and
+                      bool(np.array_equal(strict["logits"], ref[1][:len(strict["logits"])]))},
+           "reference_published": {"fpga_tok_s": 3.7, "fpga_check_max_abs_diff": 2.4e-4,
+                                   "source": "the reference README: Qwen2.5-Coder-0.5B 4-bit on the PYNQ-Z2 overlay"}}
+    log(f"drop-in (qwen.c -DFPGA on libmatvec_hip.so): {rec['value']} tok/s, FPGA_CHECK max abs diff "
+        f"{rec['fpga_check'] and rec['fpga_check']['max_abs_diff']} (strict: {timed_strict['rate']} tok/s, "
+        f"{rec['strict']['fpga_check_max_abs_diff']}, bitwise {rec['strict']['bitwise_identical_logits']})")
+    return rec
 
 
 def fast_parity(ref, prompt, ids_gpu, logits_gpu):
@@ -454,6 +510,7 @@ def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters, baselin
             f"{traffic['write_factor']:.3f})")
         main["roofline"]["traffic"] = round(traffic["fetch"] + traffic["write"])
     cpu = None if a.no_cpu else cpu_baseline(cfg, path, prompt, baseline_tokens or cpu_tokens)
+    dropin = None if a.no_cpu or name != "c3" else dropin_record(cfg, path, prompt, cpu_tokens, ref, n_logits)
     strict_rec = main if strict_main else other
     fast_rec = other if strict_main else main
     out = {
@@ -482,6 +539,8 @@ def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters, baselin
         out["fast" if strict_main else "strict"] = sub
     if ref and not strict_main:
         out["greedy_vs_reference"] = fast_parity(ref, prompt, *runs[False])
+    if dropin:
+        out["dropin"] = dropin
     return out
 
 

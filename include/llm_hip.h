@@ -13,9 +13,11 @@
  *   fast (default for .qwb): sums over groups, RMSNorm and softmax reductions run in parallel trees, so each
  *     layer output matches the reference within fp32 rounding (an int8 re-quantization that lands on the
  *     other side of a rounding boundary then moves deeper layers by more; see llm_set_strict);
- *   strict (LLM_STRICT=1 at llm_open, or llm_set_strict): every float operation in the reference's order
- *     and the reference libm's expf, so logits and token streams are bitwise those of qwen.c / runq.c
- *     built with strict IEEE flags.  llama2.c .bin GEMVs always sum their groups in order.
+ *   strict (LLM_STRICT=1 at llm_open, or llm_set_strict): every float operation of forward() in the
+ *     reference's order and the reference libm's expf, so logits and greedy token streams are bitwise those of
+ *     qwen.c / runq.c built with strict IEEE flags (the device sampler's softmax and cdf are tree sums in both
+ *     modes: sampled streams follow the reference's draws only where no probability lies within rounding of a
+ *     cut).  llama2.c .bin GEMVs always sum their groups in order.
  * Errors: -1 (or NULL) with a message on stderr, the reference's convention (matvec_fpga.h:15). */
 #pragma once
 #include <stddef.h>
@@ -147,9 +149,15 @@ int mvh_sample(const float *logits, int n, int count, float temperature, float t
 /* the prefill GEMM on caller data: y[m][r] for M tokens, weights in the reference layout (qwen planes: bits 4
  * or 8 with fp16 scales, group 32; runq: bits 0 = int8 with fp32 scales, group gs), tiled with row-blocks of
  * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d].  shape: 0 the library's choice, 10 TA + TB
- * one wave per 16 TA rows x 16 TB tokens (TA 1 or 2, TB 1, 2 or 4) */
+ * one wave per 16 TA rows x 16 TB tokens: 11, 12, 14, 21, 22, 24, 41 or 42 */
 int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
                      int bits, int gs, int rb, int shape, float *y);
+/* the GEMV launch shape the library picks for a matrix, on the host (no device needed): rows x n weights in
+ * groups of gs, wbits 4 or 8, scales fp32 (sf32 1) or fp16, row-blocks of rb rows, role 0 QKV, 1 attention output, 2 gate/up, 3 down,
+ * 4 the output head's argmax, 5 a drop-in GEMV; ordered: bit 0 groups added in order, bit 1 the strict
+ * RMSNorm; cus the device's compute units.  out[4] = waves per row-block, row-blocks per iteration, grid,
+ * ordered-in-LDS flag.  0, 1 when no shape adds this matrix's groups in order, -1 on bad arguments. */
+int mvh_gemv_shape(int rows, int n, int gs, int wbits, int sf32, int rb, int role, int ordered, int cus, int *out);
 /* mvh_sample with no device allocation: no counterpart in the reference; for callers that cannot allocate
  * device memory (tight serving loops, harnesses that forbid hipMalloc).  Same arguments, draws and RNG state as
  * mvh_sample, but every device buffer lives in a fixed array inside the library (about 9 MiB per GPU, held

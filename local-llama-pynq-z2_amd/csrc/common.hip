@@ -39,14 +39,22 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
     if (ordered) {
         // Ordered sums (runq): the unordered split when the group products of one iteration's rows fit in
         // 64 KiB of LDS (they are then added per row in group order), else one wave per 64-row block whose
-        // lanes each own a row and add its groups in order.
+        // lanes each own a row and add its groups in order.  That second form needs 64-row blocks, a wave of
+        // its own per row-block (kw 1: no RMSNorm segments, no attention merge) and free row-blocks per
+        // iteration (no SwiGLU quantization group): any other matrix whose products overflow has no ordered
+        // shape, and grid 0 says so.
         gemv_split(s, C, 4, T, epi);
         if ((size_t)s.nb * T.rb * (T.ng + 1) * 4 <= 65536) {
             s.ord = 1;
             ordered = 0; // shaped like the unordered GEMV from here on
-        } else {
+        } else if (T.rb == 64 && epi != EPI_SWIGLU && pro != PRO_ATTN && !seq_norm) {
             s.kw = 1;
             s.nb = 4;
+        } else {
+            s.kw = s.nb = 1;
+            s.grid = 0;
+            s.depth = 2;
+            return s;
         }
     } else {
         gemv_split(s, C, 4, T, epi);

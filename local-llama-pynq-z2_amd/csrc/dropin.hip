@@ -113,6 +113,11 @@ const Weight *weight(const char *who, uint64_t w, uint64_t ws, int n, int d, int
         return nullptr;
     }
     x.shape = gemv_pick_shape(x.T, PRO_XQ, EPI_STORE, ordered, hip_cu_count(S.device));
+    if (x.shape.grid < 1) {
+        fprintf(stderr, "%s: no GEMV shape for a %d x %d matrix\n", who, d, n);
+        hipFree(x.tiled);
+        return nullptr;
+    }
     return &S.weights.emplace(key, x).first->second;
 }
 

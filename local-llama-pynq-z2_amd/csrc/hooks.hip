@@ -246,3 +246,21 @@ extern "C" int mvh_ref_expf_host(const float *x, int n, float *y) {
     for (int i = 0; i < n; i++) y[i] = ref_expf_with(x[i], ref_expf_tab_host);
     return 0;
 }
+
+extern "C" int mvh_gemv_shape(int rows, int n, int gs, int wbits, int sf32, int rb, int role, int ordered, int cus,
+                              int *out) {
+    static const int pro[6] = {PRO_NORM, PRO_ATTN, PRO_NORM, PRO_XQ, PRO_NORM, PRO_XQ};
+    static const int epi[6] = {EPI_QKV, EPI_RESID, EPI_SWIGLU, EPI_RESID, EPI_ARGMAX, EPI_STORE};
+    if (!out || rows < 1 || n < 1 || (gs != 32 && gs != 64) || n % gs || (wbits != 4 && wbits != 8) ||
+        (rb != 8 && rb != 16 && rb != 32 && rb != 64) || role < 0 || role > 5 || cus < 1) {
+        fprintf(stderr, "mvh_gemv_shape: bad arguments\n");
+        return -1;
+    }
+    const TiledMat T = tiled_describe(rows, n, gs, wbits, sf32 != 0, rb);
+    const GemvShape s = gemv_pick_shape(T, pro[role], epi[role], ordered, cus);
+    out[0] = s.kw;
+    out[1] = s.nb;
+    out[2] = s.grid;
+    out[3] = s.ord;
+    return s.grid < 1 ? 1 : 0;
+}

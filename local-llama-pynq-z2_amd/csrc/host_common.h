@@ -37,7 +37,8 @@ struct GemvShape {
     int kw, nb, grid, depth;
     int ord; // ordered sums through LDS group products (GemvArgs::ord)
 };
-// ordered: bit 0 the group products summed in group order, bit 1 the strict mode's sequential RMSNorm sum
+// ordered: bit 0 the group products summed in group order, bit 1 the strict mode's sequential RMSNorm sum.
+// grid 0: no shape adds this matrix's groups in order (products beyond 64 KiB of LDS outside the 64-row form).
 GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int cus);
 
 // Compute units of device `dev` (0 with a message on failure).

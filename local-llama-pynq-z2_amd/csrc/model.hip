@@ -471,6 +471,15 @@ int pick_shapes(llm_model *m) {
         ly.s_down = gemv_pick_shape(ly.down, PRO_XQ, EPI_RESID, ord, cus);
     }
     const GemvShape h = gemv_pick_shape(m->head, PRO_NORM, EPI_ARGMAX, ord, cus);
+    for (const Layer &ly : m->L)
+        for (const auto &[sh, T] : {std::pair<const GemvShape &, const TiledMat &>{ly.s_qkv, ly.qkv}, {ly.s_o, ly.o},
+                                    {ly.s_gu, ly.gu}, {ly.s_down, ly.down}, {h, m->head}})
+            if (sh.grid < 1) {
+                fprintf(stderr, "llm: the group products of a %d x %d matrix in %d-row blocks exceed 64 KiB of LDS: "
+                        "no GEMV shape adds them in group order (%s)\n", T.rows, T.n, T.rb,
+                        m->kind == 1 ? "runq models" : "the strict mode");
+                return -1;
+            }
     if (m->part_cap && h.grid > m->part_cap) { // the argmax partials are sized at load for both modes
         fprintf(stderr, "llm: internal error: head grid %d over %d partials\n", h.grid, m->part_cap);
         return -1;
@@ -483,13 +492,15 @@ int finish_setup(llm_model *m) {
     const llm_info &I = m->info;
     if (const char *e = getenv("LLM_STRICT")) m->strict = atoi(e) != 0;
     // the argmax partials are sized for the larger of the two head grids (fast and ordered)
+    // (a .qwb too wide for ordered sums loads in the fast mode only: llm_set_strict(1) then fails)
     int head_grid = 0;
     for (int st = 0; st < 2; st++) {
         const int keep = m->strict;
         m->strict = st;
-        if (pick_shapes(m)) return -1;
-        head_grid = std::max(head_grid, m->s_head.grid);
+        const int r = pick_shapes(m);
         m->strict = keep;
+        if (r && (st == 0 || m->kind == 1 || keep)) return -1;
+        if (!r) head_grid = std::max(head_grid, m->s_head.grid);
     }
     if (pick_shapes(m)) return -1;
     // attention slices: up to 64 per kv head, each at least ATT_SUB positions
@@ -1415,7 +1426,11 @@ extern "C" int llm_set_strict(llm_model *m, int on) {
     HIP_OR_FAIL("llm_set_strict", hipStreamSynchronize(m->st));
     if ((on != 0) == (m->strict != 0)) return 0;
     m->strict = on != 0;
-    if (pick_shapes(m)) return -1;
+    if (pick_shapes(m)) {
+        m->strict = !m->strict;
+        pick_shapes(m);
+        return -1;
+    }
     // the captured step graphs hold the other mode's kernels and shapes
     for (hipGraphExec_t *g : {&m->g_plain, &m->g_hist, &m->g_plain_s, &m->g_hist_s})
         if (*g) {

@@ -2,7 +2,7 @@
 //
 // The reference processes a prompt one position at a time with the same forward() (qwen.c:674-681); no
 // batched prefill exists there (README.md:386-387).  Here the M positions of a chunk share each weight
-// read: the layer matrices become int8 MFMA GEMMs (v_mfma_i32_32x32x32_i8) over the tiled records the decode
+// read: the layer matrices become int8 MFMA GEMMs (v_mfma_i32_16x16x32_i8) over the tiled records the decode
 // GEMV reads, with the per-group int32 sums exact and the group terms p = ((float)ival * ws) * xs added in
 // group order, which is the reference's matmul (qwen.c:436-456, runq.c:429-458) for every (row, token).
 // The element-wise steps of forward() run per token, and attention is causal over the KV cache.

@@ -186,6 +186,7 @@ int main(int argc, char **argv) {
     else { fprintf(stderr, "unknown preset %s\n", p); return 1; }
     g_seed = argc > 4 ? strtoull(argv[4], NULL, 10) : 1;
     int32_t *given_ids = NULL;
+    int n_given = 0;
     for (int i = 5; i < argc; i++) {
         if (!strncmp(argv[i], "head_ids=", 9)) {
             FILE *f = fopen(argv[i] + 9, "rb");
@@ -196,10 +197,15 @@ int main(int argc, char **argv) {
             given_ids = malloc((size_t)bytes);
             if (fread(given_ids, 1, (size_t)bytes, f) != (size_t)bytes) { fprintf(stderr, "short read of %s\n", argv[i] + 9); return 1; }
             fclose(f);
-            c.head_k = (int)(bytes / 4);
+            n_given = (int)(bytes / 4);
+            c.head_k = n_given;
             continue;
         }
         if (set_key(&c, argv[i])) { fprintf(stderr, "bad override %s\n", argv[i]); return 1; }
+    }
+    if (given_ids && c.head_k != n_given) { // a head_k override next to the file: the file's count rules
+        fprintf(stderr, "head_k=%d does not match the %d ids of the head_ids file\n", c.head_k, n_given);
+        return 1;
     }
     if (given_ids)
         for (int i = 0; i < c.head_k; i++)

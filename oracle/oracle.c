@@ -206,13 +206,13 @@ void or_rmsnorm(float *o, const float *x, const float *w, int n, float eps) {
     for (int j = 0; j < n; j++) o[j] = w[j] * (ss * x[j]);
 }
 
-/* qwen.c:346-352 */
 /* expf of the C library the reference links (glibc on the hosts here), element by element: the function the
  * reference's softmax (qwen.c:350, runq.c:420) and SiLU (qwen.c:560, runq.c:592) call */
 void or_expf(const float *x, int n, float *y) {
     for (int i = 0; i < n; i++) y[i] = expf(x[i]);
 }
 
+/* qwen.c:346-352 */
 void or_softmax(float *x, int n) {
     float mx = x[0];
     for (int i = 1; i < n; i++)

@@ -229,14 +229,46 @@ def test_positions_beyond_context_are_rejected(capfd):
     m.close()
 
 
-def run_ref(binary, args):
+def run_ref(binary, args, **env_extra):
     exe = os.path.join(REF_DIR, binary)
     if not os.path.exists(exe):
         pytest.skip(f"{exe} not built")
-    env = dict(os.environ, FPGA_CHECK="1")
-    r = subprocess.run([exe, *args], capture_output=True, text=True, timeout=120, env=env)
+    env = dict(os.environ, FPGA_CHECK="1", **env_extra)
+    r = subprocess.run([exe, *args], capture_output=True, text=True, timeout=300, env=env)
     assert r.returncode == 0, r.stderr
     return r
+
+
+def fpga_check_abs(stderr):
+    """the max abs diff of the reference's own FPGA_CHECK line (qwen.c / runq.c: every matmul also on the CPU)"""
+    line = [l for l in stderr.splitlines() if l.startswith("FPGA_CHECK")][0]
+    return float(line.split("max abs diff")[1].split(",")[0]), line
+
+
+def test_reference_qwen_host_on_the_dropin_library_at_the_qwen2_0_5b_shape(tmp_path):
+    """the reference's qwen.c built with -DFPGA against libmatvec_hip.so on a Qwen2-0.5B-shape .qwb (24 layers,
+    896 wide, Q4_0 layers, the 65536-row Q8_0 head in the reference's 2048-row head blocks, its 8 MiB weight
+    chunks): with LLM_STRICT=1 every fpga_matvec4 adds a row's groups in order, so the logits of every position
+    equal the reference CPU build's bit for bit and FPGA_CHECK reads 0; in the default mode (the testbench's bar)
+    the ids are the CPU build's and FPGA_CHECK stays far below the reference's own published 2.4e-4"""
+    from test_lib import walk_qwb
+    p = synth("qwb", str(tmp_path / "c3.qwb"), "c3", 41)
+    w = walk_qwb(p)
+    head_ids, head_k = w["head_ids"], w["cfg"][6]
+    prompt = [int(v) for v in np.random.default_rng(42).choice(head_ids, 24, replace=False)]
+    args = [p, "--ids", ",".join(map(str, prompt)), "-t", "0", "-n", "8", "-c", "64"]
+    cpu = run_ref("qwen", args + ["--logits", str(tmp_path / "cpu.bin")])
+    ref = np.fromfile(str(tmp_path / "cpu.bin"), "<f4").reshape(-1, head_k)
+    strict = run_ref("qwen-hip", args + ["--logits", str(tmp_path / "hip.bin")], LLM_STRICT="1")
+    got = np.fromfile(str(tmp_path / "hip.bin"), "<f4").reshape(-1, head_k)
+    assert strict.stdout == cpu.stdout and len(ref) == 24 + 7
+    assert np.array_equal(got, ref)
+    diff, line = fpga_check_abs(strict.stderr)
+    assert diff == 0.0, line
+    fast = run_ref("qwen-hip", args)
+    diff, line = fpga_check_abs(fast.stderr)
+    assert fast.stdout == cpu.stdout
+    assert diff < 1e-4, line
 
 
 def test_reference_qwen_host_on_the_dropin_library(tmp_path):

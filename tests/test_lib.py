@@ -43,6 +43,44 @@ def test_calls_before_open_fail_like_the_reference(capfd):
     L.fpga_close()
 
 
+def gemv_shape(rows, n, gs, wbits, sf32, rb, role, ordered, cus=256):
+    import ctypes as C
+    out = (C.c_int * 4)()
+    rc = pkg().lib().mvh_gemv_shape(rows, n, gs, wbits, sf32, rb, role, ordered, cus, out)
+    return rc, tuple(out)
+
+
+@pytest.mark.parametrize("name,dims,gs,wbits,sf32,rb,role,ordered", [
+    ("runq 4096 gate/up", (2 * 11008, 4096), 64, 8, 1, 8, 2, 1),
+    ("runq 4096 down", (4096, 11008), 64, 8, 1, 8, 3, 1),
+    ("runq 8192 qkv", (8192 + 2 * 1024, 8192), 64, 8, 1, 8, 0, 1),
+    ("qwen 896 strict gate/up", (2 * 4864, 896), 32, 4, 0, 16, 2, 3),
+    ("qwen 3584 strict down", (3584, 18944), 32, 4, 0, 8, 3, 3),
+    ("qwen 3584 strict head", (65536, 3584), 32, 8, 0, 16, 4, 3),
+    ("qwen 8192 strict qkv", (8192 + 2 * 1024, 8192), 32, 4, 0, 16, 0, 3),
+])
+def test_ordered_gemv_shapes_keep_their_products_in_lds(name, dims, gs, wbits, sf32, rb, role, ordered):
+    """every ordered shape the library picks adds each row's group products in group order from LDS: one
+    iteration's products (nb row-blocks x rb rows x ng + 1 padded groups of fp32) within 64 KiB"""
+    rows, n = dims
+    rc, (kw, nb, grid, ordq) = gemv_shape(rows, n, gs, wbits, sf32, rb, role, ordered)
+    assert rc == 0 and grid >= 1 and ordq == 1, (name, kw, nb, grid, ordq)
+    assert nb * rb * (n // gs + 1) * 4 <= 65536, name
+
+
+def test_ordered_gemv_without_an_ordered_shape_is_refused():
+    """a gate/up whose SwiGLU epilogue fixes the row-blocks per iteration (gs / (rb / 2)) with too many groups
+    for LDS has no ordered shape: llama2.c .bin at dim 8192 (8-row blocks, groups of 64) and a .qwb at dim
+    8192 in the strict mode (16-row blocks, groups of 32) are refused (grid 0), not summed out of order; the
+    same .qwb matrix in the fast mode and a drop-in GEMV (64-row blocks, one row per lane) keep a shape"""
+    assert gemv_shape(2 * 28672, 8192, 64, 8, 1, 8, 2, 1)[0] == 1
+    assert gemv_shape(2 * 29568, 8192, 32, 4, 0, 16, 2, 3)[0] == 1
+    assert gemv_shape(2 * 29568, 8192, 32, 4, 0, 16, 2, 0)[0] == 0
+    rc, (kw, nb, grid, ordq) = gemv_shape(4096, 65536, 32, 4, 0, 64, 5, 1)
+    assert rc == 0 and kw == 1 and ordq == 0 and grid >= 1
+    assert gemv_shape(4096, 4096, 48, 4, 0, 64, 5, 1)[0] == -1
+
+
 def test_synth_is_deterministic(tmp_path):
     for fmt, name in (("qwb", "tiny.qwb"), ("bin", "tiny.bin")):
         p = synth(fmt, str(tmp_path / name), "tiny", 1)
