@@ -1,28 +1,31 @@
-/* Qwen2 / Qwen2.5 byte-level BPE tokenizer (interface: qwen_tokenizer.h).
+/* Qwen2 / Qwen2.5 byte-level BPE tokenizer of the C hosts (interface: qwen_tokenizer.h).
  *
- * Data file "QWTOK001" (the reference's format, tools/qwen_tok_export.py:21-41; little-endian, every
- * section padded to 4 bytes):
- *   magic[8], u32 hdr[12] = n_vocab, n_added, n_merges, blob_len, n_uni, n_dec, dec_pool_len, n_comp, 0...
- *   u8 tok_len[n_vocab], u8 blob[blob_len], u32 merges[n_merges][3] (left, right, merged; index = rank),
- *   n_added x (u32 id, u32 len, text[len]), u32 uni[n_uni] (run-length: start | payload << 21, payload =
- *   class (0 other, 1 letter, 2 number, 3 white space) | NFC-may-change << 2 | combining class << 3),
- *   u32 dec_cp[n_dec], dec_off[n_dec + 1], dec_pool[dec_pool_len] (full canonical decompositions),
- *   u32 comp[n_comp][3] (first, second, composite) sorted by (first, second).
+ * Data: the "QWTOK001" file that the reference's tools/qwen_tok_export.py:21-41 writes (little-endian, every
+ * section zero-padded to 4 bytes):
+ *   magic[8], u32 hdr[12] = n_vocab, n_added, n_merges, blob_len, n_uni, n_dec, dec_pool_len, n_comp, 0...;
+ *   u8 tok_len[n_vocab]; u8 blob[blob_len] (token bytes in id order); u32 merges[n_merges][3] (left, right,
+ *   merged; the index is the merge rank); n_added x (u32 id, u32 len, u8 text[len]); u32 uni[n_uni] (runs of
+ *   code points: start | payload << 21, payload = class (0 other, 1 letter, 2 number, 3 white space) |
+ *   "NFC may change the text here" << 2 | canonical combining class << 3); u32 dec_cp[n_dec],
+ *   dec_off[n_dec + 1], dec_pool[] (full canonical decompositions); u32 comp[n_comp][3] (first, second,
+ *   composite).
  *
- * Encoding (what Hugging Face `tokenizers` does for Qwen2.5, qwen/tokenizer.c:1-12 states the same pipeline):
- *   1. split the text at added tokens (when allowed): the leftmost position where one starts, the longest
- *      one there;
- *   2. NFC each piece between them.  Only maximal runs of non-ASCII characters that hold a character the
- *      table marks as possibly changed by NFC are rewritten, together with the ASCII character before the
- *      run (an ASCII letter can take a combining mark); everything else is left as it is;
- *   3. the pre-tokenizer regex of Qwen2
+ * tok_encode gives the ids of Hugging Face `tokenizers` for the Qwen2 tokenizer.json:
+ *   1. with allow_special, added tokens are cut out of the raw text: at the leftmost position where one
+ *      starts, the longest one there;
+ *   2. every span between them is put in NFC (UAX #15).  The span is cut before each "quiet" code point (a
+ *      starter that NFC leaves alone and that never composes with what precedes it); only the pieces holding
+ *      another code point are decomposed, reordered and recomposed;
+ *   3. the normalized span is cut into pre-tokens by the Qwen2 Split regex
  *        (?i:'s|'t|'re|'ve|'m|'ll|'d) | [^\r\n\p{L}\p{N}]?\p{L}+ | \p{N} | ?[^\s\p{L}\p{N}]+[\r\n]* |
  *        \s*[\r\n]+ | \s+(?!\S) | \s+
- *      evaluated by hand with the outcome of a backtracking engine (first alternative that matches, greedy);
- *   4. each pre-token's bytes become single-byte tokens, merged by BPE: the pair of lowest merge rank first,
- *      the leftmost of equal ranks, until no pair has a merge.
- * Bytes that are not valid UTF-8 are kept as they are: class "other", never normalized.
- * Not thread-safe (scratch buffers live in the Tokenizer). */
+ *      as a table of seven matchers over classified code points, tried in that order, each returning what a
+ *      backtracking engine's greedy match of that alternative consumes;
+ *   4. each pre-token's UTF-8 bytes start as the 256 single-byte tokens and are merged by BPE: the adjacent
+ *      pair of lowest merge rank, the leftmost one among equal ranks, found with a min-tree over the pairs.
+ * Bytes that are not UTF-8 become one-byte units of class "other" that normalization never touches.
+ * One open-addressing hash map type serves the merges, the decompositions and the compositions.
+ * Not thread-safe: a Tokenizer owns its scratch memory. */
 #include "qwen_tokenizer.h"
 
 #include <stdint.h>
@@ -30,400 +33,455 @@
 #include <stdlib.h>
 #include <string.h>
 
-enum { CL_OTHER = 0, CL_LETTER = 1, CL_NUMBER = 2, CL_SPACE = 3 };
-#define NOT_UTF8 0x110000u /* a byte b that does not decode stands for the code point NOT_UTF8 + b */
+enum { K_OTHER = 0, K_LETTER = 1, K_NUMBER = 2, K_SPACE = 3 };
+#define PAY_DIRTY 4u
+#define PSEUDO 0x110000u /* an undecodable byte b is the unit PSEUDO + b */
+#define NO_PAIR UINT64_MAX
 
-typedef struct {
-    uint32_t id, len;
-    const char *text;
-} Special;
+/* Hangul syllables (Unicode ch. 3.12) */
+#define H_S 0xAC00u
+#define H_L 0x1100u
+#define H_V 0x1161u
+#define H_T 0x11A7u
+#define H_VN 21u
+#define H_TN 28u
+#define H_SN 11172u
 
-typedef struct {
-    uint32_t rank, pos; /* queue order: rank, then position */
-    int32_t left, right; /* the symbol ids the pair had when queued */
-} Cand;
+/* ---- growable scratch ---------------------------------------------------------------------------------- */
 
 typedef struct {
     void *p;
-    size_t n, cap;
-} Grow;
+    size_t cap;
+} Scratch;
 
-struct Tokenizer {
-    uint8_t *file;
-    uint32_t n_vocab, n_added, n_merges, n_ids;
-    const uint8_t *tlen, *blob;
-    uint32_t *toff;                 /* n_vocab + 1 byte offsets into blob */
-    const uint32_t *merges;         /* [rank][3] */
-    uint64_t *mkey;                 /* merge table, open addressing: key = left << 32 | right, 0 = empty */
-    uint32_t *mval;                 /* rank of the key at the same slot */
-    uint32_t mmask;
-    Special *spec;
-    uint8_t spec_lead[256];
-    uint32_t n_uni, n_dec, n_comp, pool_len;
-    const uint32_t *uni, *dec_cp, *dec_off, *dec_pool, *comp;
-    int32_t byte_tok[256];
-    uint8_t ascii_cls[128];
-    uint32_t hit_lo, hit_hi, hit_val; /* last run looked up: [hit_lo, hit_hi) -> payload */
-    /* scratch */
-    Grow cps, marks, out, sym, queue;
-};
+static void *reserve(Scratch *s, size_t bytes) {
+    if (bytes > s->cap) {
+        size_t c = s->cap ? s->cap : 4096;
+        while (c < bytes) c *= 2;
+        void *q = realloc(s->p, c);
+        if (!q) return NULL;
+        s->p = q;
+        s->cap = c;
+    }
+    return s->p;
+}
 
-static int grow(Grow *g, size_t want, size_t elem) {
-    if (want <= g->cap) return 0;
-    size_t c = g->cap ? g->cap : 64;
-    while (c < want) c *= 2;
-    void *q = realloc(g->p, c * elem);
-    if (!q) return -1;
-    g->p = q;
-    g->cap = c;
+/* ---- 64-bit key -> 32-bit value map (linear probing, keys never equal to EMPTY) -------------------------- */
+
+#define EMPTY UINT64_MAX
+
+typedef struct {
+    uint64_t *key;
+    uint32_t *val;
+    size_t mask;
+} Map;
+
+static size_t slot_of(uint64_t k, size_t mask) {
+    k ^= k >> 33;
+    k *= 0xFF51AFD7ED558CCDull;
+    k ^= k >> 29;
+    return (size_t)k & mask;
+}
+
+static int map_init(Map *m, size_t entries) {
+    size_t cap = 64;
+    while (cap < entries * 2) cap *= 2;
+    m->key = malloc(cap * sizeof *m->key);
+    m->val = malloc(cap * sizeof *m->val);
+    m->mask = cap - 1;
+    if (!m->key || !m->val) return -1;
+    memset(m->key, 0xFF, cap * sizeof *m->key);
     return 0;
 }
 
-/* ------------------------------------------------------------------------------------------------------
- * UTF-8 and the Unicode table */
+/* keeps the first value given for a key */
+static void map_put(Map *m, uint64_t k, uint32_t v) {
+    size_t i = slot_of(k, m->mask);
+    while (m->key[i] != EMPTY) {
+        if (m->key[i] == k) return;
+        i = (i + 1) & m->mask;
+    }
+    m->key[i] = k;
+    m->val[i] = v;
+}
 
-/* one character of s[0..n): its length, the code point in *cp (NOT_UTF8 + byte for a byte that does not
- * start a well-formed character: overlong forms, surrogates and values past U+10FFFF included) */
-static int utf8_next(const uint8_t *s, size_t n, uint32_t *cp) {
+static int64_t map_get(const Map *m, uint64_t k) {
+    for (size_t i = slot_of(k, m->mask);; i = (i + 1) & m->mask) {
+        if (m->key[i] == k) return m->val[i];
+        if (m->key[i] == EMPTY) return -1;
+    }
+}
+
+static void map_free(Map *m) {
+    free(m->key);
+    free(m->val);
+}
+
+/* ---- the tokenizer ---------------------------------------------------------------------------------------- */
+
+typedef struct {
+    uint32_t cp;  /* code point, or PSEUDO + byte */
+    uint32_t off; /* byte offset in the span */
+    uint16_t pay; /* Unicode payload */
+    uint8_t len;  /* bytes */
+} Unit;
+
+typedef struct {
+    uint32_t cp, ccc;
+} Mark;
+
+struct Tokenizer {
+    uint8_t *data; /* the whole file: pieces, merges, added texts and Unicode tables point into it */
+    uint32_t n_base, n_ids, n_added, n_runs;
+    uint32_t *piece_at;  /* [n_ids] offset of the id's bytes in data */
+    uint16_t *piece_len; /* [n_ids] their length, 0 where no id exists */
+    const uint32_t *merges, *runs, *dec_off, *dec_pool;
+    uint32_t *added_ids; /* added token ids, longest text first */
+    uint8_t lead[32];    /* bitmap of the added tokens' first bytes */
+    int32_t byte_tok[256];
+    uint16_t low_pay[256]; /* payload of U+0000 .. U+00FF */
+    Map pair_rank;         /* (left << 32 | right) -> merge rank */
+    Map decomp;            /* code point -> index into dec_off */
+    Map compose;           /* (first << 32 | second) -> composite */
+    Scratch norm, units, marks, sym, tree, out;
+};
+
+/* the payload of the last run that starts at or before cp (runs[0] starts at 0) */
+static uint32_t run_payload(const Tokenizer *t, uint32_t cp) {
+    const uint32_t *r = t->runs;
+    size_t n = t->n_runs;
+    while (n > 1) {
+        const size_t half = n / 2;
+        if ((r[half] & 0x1FFFFF) <= cp) r += half;
+        n -= half;
+    }
+    return *r >> 21;
+}
+
+static uint32_t payload(const Tokenizer *t, uint32_t cp) {
+    if (cp < 256) return t->low_pay[cp];
+    return cp >= PSEUDO ? 0 : run_payload(t, cp);
+}
+
+static inline unsigned unit_class(const Unit *u) { return u->pay & 3u; }
+static inline int is_dirty(const Unit *u) { return (u->pay & PAY_DIRTY) != 0; }
+static inline int is_crlf(uint32_t cp) { return cp == '\r' || cp == '\n'; }
+
+/* One code point at s[0 .. n): its length in bytes.  Overlong forms, surrogates, values past U+10FFFF and cut
+ * sequences come back one byte at a time as PSEUDO + byte. */
+static int utf8_unit(const uint8_t *s, size_t n, uint32_t *cp) {
+    static const uint8_t tail[16] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 2, 3};
+    static const uint32_t least[4] = {0, 0x80, 0x800, 0x10000};
     const uint32_t b = s[0];
+    const int k = tail[b >> 4];
     if (b < 0x80) {
         *cp = b;
         return 1;
     }
-    int need;
-    uint32_t v, min;
-    if (b >= 0xC2 && b <= 0xDF) { need = 1; v = b & 0x1F; min = 0x80; }
-    else if (b >= 0xE0 && b <= 0xEF) { need = 2; v = b & 0x0F; min = 0x800; }
-    else if (b >= 0xF0 && b <= 0xF4) { need = 3; v = b & 0x07; min = 0x10000; }
-    else { *cp = NOT_UTF8 + b; return 1; }
-    if ((size_t)need >= n) { *cp = NOT_UTF8 + b; return 1; }
-    for (int k = 1; k <= need; k++) {
-        if ((s[k] & 0xC0) != 0x80) { *cp = NOT_UTF8 + b; return 1; }
-        v = v << 6 | (s[k] & 0x3F);
-    }
-    if (v < min || v > 0x10FFFF || (v >= 0xD800 && v <= 0xDFFF)) { *cp = NOT_UTF8 + b; return 1; }
-    *cp = v;
-    return need + 1;
-}
-
-static int utf8_put(Grow *o, uint32_t cp) {
-    if (grow(o, o->n + 4, 1)) return -1;
-    uint8_t *d = (uint8_t *)o->p + o->n;
-    if (cp >= NOT_UTF8) { d[0] = (uint8_t)(cp - NOT_UTF8); o->n += 1; }
-    else if (cp < 0x80) { d[0] = (uint8_t)cp; o->n += 1; }
-    else if (cp < 0x800) { d[0] = (uint8_t)(0xC0 | cp >> 6); d[1] = (uint8_t)(0x80 | (cp & 0x3F)); o->n += 2; }
-    else if (cp < 0x10000) {
-        d[0] = (uint8_t)(0xE0 | cp >> 12); d[1] = (uint8_t)(0x80 | (cp >> 6 & 0x3F)); d[2] = (uint8_t)(0x80 | (cp & 0x3F));
-        o->n += 3;
-    } else {
-        d[0] = (uint8_t)(0xF0 | cp >> 18); d[1] = (uint8_t)(0x80 | (cp >> 12 & 0x3F));
-        d[2] = (uint8_t)(0x80 | (cp >> 6 & 0x3F)); d[3] = (uint8_t)(0x80 | (cp & 0x3F));
-        o->n += 4;
-    }
-    return 0;
-}
-
-static uint32_t payload(Tokenizer *t, uint32_t cp) {
-    if (cp >= NOT_UTF8) return 0;
-    if (cp >= t->hit_lo && cp < t->hit_hi) return t->hit_val;
-    uint32_t lo = 0, hi = t->n_uni; /* the last run starting at or before cp (the first starts at 0) */
-    while (hi - lo > 1) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if ((t->uni[mid] & 0x1FFFFF) <= cp) lo = mid;
-        else hi = mid;
-    }
-    t->hit_lo = t->uni[lo] & 0x1FFFFF;
-    t->hit_hi = lo + 1 < t->n_uni ? (t->uni[lo + 1] & 0x1FFFFF) : NOT_UTF8;
-    t->hit_val = t->uni[lo] >> 21;
-    return t->hit_val;
-}
-
-static unsigned char_class(Tokenizer *t, uint32_t cp) { return cp < 128 ? t->ascii_cls[cp] : payload(t, cp) & 3; }
-static unsigned comb_class(Tokenizer *t, uint32_t cp) { return payload(t, cp) >> 3 & 0xFF; }
-
-/* ------------------------------------------------------------------------------------------------------
- * NFC (Unicode Standard Annex 15): canonical decomposition, canonical ordering, canonical composition.
- * Hangul syllables are decomposed and composed arithmetically (Unicode 3.12); the rest uses the tables. */
-
-enum { H_SBASE = 0xAC00, H_LBASE = 0x1100, H_VBASE = 0x1161, H_TBASE = 0x11A7, H_LCOUNT = 19, H_VCOUNT = 21,
-       H_TCOUNT = 28, H_NCOUNT = H_VCOUNT * H_TCOUNT, H_SCOUNT = H_LCOUNT * H_NCOUNT };
-
-static int push_cp(Grow *g, uint32_t cp) {
-    if (grow(g, g->n + 1, sizeof(uint32_t))) return -1;
-    ((uint32_t *)g->p)[g->n++] = cp;
-    return 0;
-}
-
-static int decompose_into(Tokenizer *t, uint32_t cp, Grow *g) {
-    if (cp >= H_SBASE && cp < H_SBASE + H_SCOUNT) {
-        const uint32_t s = cp - H_SBASE;
-        if (push_cp(g, H_LBASE + s / H_NCOUNT) || push_cp(g, H_VBASE + s % H_NCOUNT / H_TCOUNT)) return -1;
-        return s % H_TCOUNT ? push_cp(g, H_TBASE + s % H_TCOUNT) : 0;
-    }
-    uint32_t lo = 0, hi = t->n_dec;
-    while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        if (t->dec_cp[mid] < cp) lo = mid + 1;
-        else hi = mid;
-    }
-    if (lo < t->n_dec && t->dec_cp[lo] == cp) {
-        for (uint32_t k = t->dec_off[lo]; k < t->dec_off[lo + 1]; k++)
-            if (push_cp(g, t->dec_pool[k])) return -1;
-        return 0;
-    }
-    return push_cp(g, cp);
-}
-
-static uint32_t compose(const Tokenizer *t, uint32_t a, uint32_t b) {
-    if (a >= H_LBASE && a < H_LBASE + H_LCOUNT && b >= H_VBASE && b < H_VBASE + H_VCOUNT)
-        return H_SBASE + ((a - H_LBASE) * H_VCOUNT + (b - H_VBASE)) * H_TCOUNT;
-    if (a >= H_SBASE && a < H_SBASE + H_SCOUNT && (a - H_SBASE) % H_TCOUNT == 0 && b > H_TBASE &&
-        b < H_TBASE + H_TCOUNT)
-        return a + (b - H_TBASE);
-    uint32_t lo = 0, hi = t->n_comp;
-    while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        const uint32_t *e = t->comp + 3 * (size_t)mid;
-        if (e[0] < a || (e[0] == a && e[1] < b)) lo = mid + 1;
-        else hi = mid;
-    }
-    const uint32_t *e = t->comp + 3 * (size_t)lo;
-    return lo < t->n_comp && e[0] == a && e[1] == b ? e[2] : 0;
-}
-
-/* NFC of the code points src[0..n), appended to t->out as UTF-8 */
-static int nfc_append(Tokenizer *t, const uint32_t *src, size_t n) {
-    Grow *d = &t->marks; /* decomposed code points, then their combining classes after them */
-    d->n = 0;
-    for (size_t i = 0; i < n; i++)
-        if (decompose_into(t, src[i], d)) return -1;
-    const size_t m = d->n;
-    if (grow(d, 2 * m, sizeof(uint32_t))) return -1;
-    uint32_t *c = (uint32_t *)d->p, *cc = c + m;
-    for (size_t i = 0; i < m; i++) cc[i] = comb_class(t, c[i]);
-    /* canonical ordering: a stable sort of each run of non-starters by combining class */
-    for (size_t i = 1; i < m; i++) {
-        const uint32_t x = c[i], k = cc[i];
-        if (!k) continue;
-        size_t j = i;
-        for (; j > 0 && cc[j - 1] > k; j--) { c[j] = c[j - 1]; cc[j] = cc[j - 1]; }
-        c[j] = x;
-        cc[j] = k;
-    }
-    /* canonical composition: a character joins the last starter unless something in between blocks it
-     * (after the ordering, only the character just before it can) */
-    size_t w = 0, starter = (size_t)-1;
-    for (size_t i = 0; i < m; i++) {
-        const uint32_t x = c[i], k = cc[i];
-        if (starter != (size_t)-1 && (w - 1 == starter || (cc[w - 1] != 0 && cc[w - 1] < k))) {
-            const uint32_t y = compose(t, c[starter], x);
-            if (y) {
-                c[starter] = y;
-                continue;
-            }
+    if (k && (size_t)k < n && b < 0xF5) {
+        uint32_t v = b & (0x3Fu >> k);
+        int i = 1;
+        for (; i <= k && (s[i] & 0xC0) == 0x80; i++) v = v << 6 | (s[i] & 0x3F);
+        if (i > k && v >= least[k] && v < PSEUDO && (v & 0xFFFFF800u) != 0xD800u) {
+            *cp = v;
+            return k + 1;
         }
-        if (k == 0) starter = w;
-        c[w] = x;
-        cc[w] = k;
-        w++;
     }
-    for (size_t i = 0; i < w; i++)
-        if (utf8_put(&t->out, c[i])) return -1;
-    return 0;
+    *cp = PSEUDO + b;
+    return 1;
 }
 
-/* NFC of s[0..n): s itself when nothing changes, else t->out's bytes; NULL when out of memory */
-static const uint8_t *normalize(Tokenizer *t, const uint8_t *s, size_t n, size_t *outn) {
-    size_t copied = 0; /* s[0..copied) is in t->out already (once t->out is in use) */
-    int used = 0;
+static size_t utf8_write(uint8_t *o, uint32_t cp) {
+    if (cp >= PSEUDO) {
+        o[0] = (uint8_t)(cp - PSEUDO);
+        return 1;
+    }
+    if (cp < 0x80) {
+        o[0] = (uint8_t)cp;
+        return 1;
+    }
+    size_t n = cp < 0x800 ? 2 : cp < 0x10000 ? 3 : 4;
+    for (size_t i = n - 1; i > 0; i--, cp >>= 6) o[i] = (uint8_t)(0x80 | (cp & 0x3F));
+    o[0] = (uint8_t)((0xF00u >> n) | cp); /* 2: 0xC0, 3: 0xE0, 4: 0xF0 lead bits */
+    return n;
+}
+
+/* the units of s[0 .. n) into t->units; NULL when out of memory */
+static Unit *split_units(Tokenizer *t, const uint8_t *s, size_t n, size_t *count) {
+    Unit *u = reserve(&t->units, (n + 1) * sizeof(Unit));
+    if (!u) return NULL;
+    size_t k = 0;
+    for (size_t i = 0; i < n; k++) {
+        const int l = utf8_unit(s + i, n - i, &u[k].cp);
+        u[k].off = (uint32_t)i;
+        u[k].len = (uint8_t)l;
+        u[k].pay = (uint16_t)payload(t, u[k].cp);
+        i += (size_t)l;
+    }
+    *count = k;
+    return u;
+}
+
+/* ---- NFC ------------------------------------------------------------------------------------------------ */
+
+static uint32_t ccc_of(const Tokenizer *t, uint32_t cp) { return payload(t, cp) >> 3 & 0xFF; }
+
+static uint32_t composite(const Tokenizer *t, uint32_t a, uint32_t b) {
+    if (a - H_L < 19 && b - H_V < H_VN) return H_S + ((a - H_L) * H_VN + (b - H_V)) * H_TN;
+    if (a - H_S < H_SN && (a - H_S) % H_TN == 0 && b - H_T - 1 < H_TN - 1) return a + (b - H_T);
+    const int64_t c = map_get(&t->compose, (uint64_t)a << 32 | b);
+    return c < 0 ? 0 : (uint32_t)c;
+}
+
+/* appends the canonical decomposition of cp to m (room for 4 code points); returns the new count */
+static size_t decompose(const Tokenizer *t, uint32_t cp, Mark *m, size_t k) {
+    if (cp - H_S < H_SN) {
+        const uint32_t s = cp - H_S;
+        m[k++].cp = H_L + s / (H_VN * H_TN);
+        m[k++].cp = H_V + s % (H_VN * H_TN) / H_TN;
+        if (s % H_TN) m[k++].cp = H_T + s % H_TN;
+        return k;
+    }
+    const int64_t e = cp < PSEUDO ? map_get(&t->decomp, cp) : -1;
+    if (e < 0) {
+        m[k++].cp = cp;
+        return k;
+    }
+    for (uint32_t i = t->dec_off[e]; i < t->dec_off[e + 1]; i++) m[k++].cp = t->dec_pool[i];
+    return k;
+}
+
+/* NFC of the units u[0 .. k) appended to o; returns the bytes written (at most 4 per code point) */
+static size_t nfc_piece(Tokenizer *t, const Unit *u, size_t k, uint8_t *o, Mark *m) {
+    size_t n = 0;
+    for (size_t i = 0; i < k; i++) n = decompose(t, u[i].cp, m, n);
+    for (size_t i = 0; i < n; i++) m[i].ccc = m[i].cp < PSEUDO ? ccc_of(t, m[i].cp) : 0;
+    /* canonical order: every run of non-starters sorted by combining class, equal classes kept in order */
     for (size_t i = 0; i < n;) {
-        if (s[i] < 0x80) { i++; continue; }
-        size_t e = i;
-        int dirty = 0;
-        while (e < n && s[e] >= 0x80) {
-            uint32_t cp;
-            e += (size_t)utf8_next(s + e, n - e, &cp);
-            if (payload(t, cp) & 4) dirty = 1;
+        if (!m[i].ccc) {
+            i++;
+            continue;
         }
-        if (dirty) {
-            const size_t from = i > 0 ? i - 1 : i; /* the ASCII character before the run joins it */
-            if (!used) { t->out.n = 0; used = 1; }
-            if (grow(&t->out, t->out.n + (from - copied), 1)) return NULL;
-            memcpy((uint8_t *)t->out.p + t->out.n, s + copied, from - copied);
-            t->out.n += from - copied;
-            t->cps.n = 0;
-            for (size_t k = from; k < e;) {
-                uint32_t cp;
-                k += (size_t)utf8_next(s + k, e - k, &cp);
-                if (push_cp(&t->cps, cp)) return NULL;
-            }
-            if (nfc_append(t, (const uint32_t *)t->cps.p, t->cps.n)) return NULL;
-            copied = e;
+        size_t e = i;
+        while (e < n && m[e].ccc) e++;
+        for (size_t a = i + 1; a < e; a++) {
+            const Mark x = m[a];
+            size_t b = a;
+            for (; b > i && m[b - 1].ccc > x.ccc; b--) m[b] = m[b - 1];
+            m[b] = x;
         }
         i = e;
     }
-    if (!used) { *outn = n; return s; }
-    if (grow(&t->out, t->out.n + (n - copied), 1)) return NULL;
-    memcpy((uint8_t *)t->out.p + t->out.n, s + copied, n - copied);
-    t->out.n += n - copied;
-    *outn = t->out.n;
-    return (const uint8_t *)t->out.p;
-}
-
-/* ------------------------------------------------------------------------------------------------------
- * pre-tokenizer: the end of the pre-token starting at s[i] (i < n) */
-
-/* length of the contraction after an apostrophe at s[0..n) (case-insensitive s t m d re ve ll; the long s
- * U+017F folds to s under the (?i) of the regex), 0 if none */
-static size_t contraction_len(const uint8_t *s, size_t n) {
-    if (n == 0) return 0;
-    const int c = s[0] | 0x20;
-    if (c == 's' || c == 't' || c == 'm' || c == 'd') return 1;
-    if (n >= 2 && ((c == 'r' || c == 'v') && (s[1] | 0x20) == 'e')) return 2;
-    if (n >= 2 && c == 'l' && (s[1] | 0x20) == 'l') return 2;
-    if (n >= 2 && s[0] == 0xC5 && s[1] == 0xBF) return 2;
-    return 0;
-}
-
-static size_t skip_class(Tokenizer *t, const uint8_t *s, size_t j, size_t n, unsigned cls) {
-    while (j < n) {
-        uint32_t cp;
-        const int l = utf8_next(s + j, n - j, &cp);
-        if (char_class(t, cp) != cls) break;
-        j += (size_t)l;
-    }
-    return j;
-}
-
-static size_t pretoken_end(Tokenizer *t, const uint8_t *s, size_t i, size_t n) {
-    uint32_t c, d;
-    const size_t l = (size_t)utf8_next(s + i, n - i, &c);
-    const unsigned k = char_class(t, c);
-    size_t j;
-    /* 1. 's 't 're 've 'm 'll 'd */
-    if (c == '\'' && (j = contraction_len(s + i + 1, n - i - 1)) > 0) return i + 1 + j;
-    /* 2. [^\r\n\p{L}\p{N}]?\p{L}+ : letters, possibly after one character that is none of those */
-    if (k == CL_LETTER) return skip_class(t, s, i + l, n, CL_LETTER);
-    if (c != '\r' && c != '\n' && k != CL_NUMBER && i + l < n) {
-        const size_t l2 = (size_t)utf8_next(s + i + l, n - i - l, &d);
-        if (char_class(t, d) == CL_LETTER) return skip_class(t, s, i + l + l2, n, CL_LETTER);
-    }
-    /* 3. \p{N} : one digit */
-    if (k == CL_NUMBER) return i + l;
-    /* 4.  ?[^\s\p{L}\p{N}]+[\r\n]* : an optional space, other characters, trailing line breaks */
-    j = c == ' ' ? i + 1 : i;
-    if (j < n) {
-        const size_t l2 = (size_t)utf8_next(s + j, n - j, &d);
-        if (char_class(t, d) == CL_OTHER) {
-            j = skip_class(t, s, j + l2, n, CL_OTHER);
-            while (j < n && (s[j] == '\r' || s[j] == '\n')) j++;
-            return j;
+    /* canonical composition: a mark joins the last starter unless something between blocks it */
+    size_t w = 0, bytes = 0;
+    long st = -1;
+    for (size_t i = 0; i < n; i++) {
+        const Mark x = m[i];
+        if (st >= 0) {
+            const int adjacent = (size_t)st == w - 1;
+            if (adjacent || m[w - 1].ccc < x.ccc) {
+                const uint32_t c = composite(t, m[st].cp, x.cp);
+                if (c) {
+                    m[st].cp = c;
+                    continue;
+                }
+            }
         }
+        if (!x.ccc) st = (long)w;
+        m[w++] = x;
     }
-    /* c is white space: W = the maximal white-space run starting at i */
-    size_t end = i, last = i, after_nl = 0;
-    while (end < n) {
-        const size_t l2 = (size_t)utf8_next(s + end, n - end, &d);
-        if (char_class(t, d) != CL_SPACE) break;
-        last = end;
-        if (d == '\r' || d == '\n') after_nl = end + l2;
-        end += l2;
-    }
-    if (after_nl) return after_nl; /* 5. \s*[\r\n]+ : through W's last line break */
-    if (end == n) return end;      /* 6. \s+(?!\S) : all of W at the end of the text, */
-    if (last > i) return last;     /*    else W without its last character */
-    return end;                    /* 7. \s+ */
+    for (size_t i = 0; i < w; i++) bytes += utf8_write(o + bytes, m[i].cp);
+    return bytes;
 }
 
-/* ------------------------------------------------------------------------------------------------------
- * BPE over one pre-token */
-
-static uint64_t pair_key(uint32_t a, uint32_t b) { return (uint64_t)a << 32 | b; }
-static uint32_t slot_of(uint64_t key, uint32_t mask) {
-    uint64_t h = (key + 1) * 0x9E3779B97F4A7C15ull;
-    return (uint32_t)(h >> 40) & mask;
-}
-
-static int rank_of(const Tokenizer *t, int32_t a, int32_t b) {
-    const uint64_t key = pair_key((uint32_t)a, (uint32_t)b) + 1; /* +1: key 0 marks an empty slot */
-    for (uint32_t h = slot_of(key, t->mmask);; h = (h + 1) & t->mmask) {
-        if (t->mkey[h] == 0) return -1;
-        if (t->mkey[h] == key) return (int)t->mval[h];
+/* NFC of s[0 .. n): s itself when nothing can change, else t->norm; NULL when out of memory */
+static const uint8_t *nfc(Tokenizer *t, const uint8_t *s, size_t n, size_t *out_n) {
+    size_t nu;
+    Unit *u = split_units(t, s, n, &nu);
+    if (!u) return NULL;
+    size_t first = 0;
+    while (first < nu && !is_dirty(&u[first])) first++;
+    if (first == nu) {
+        *out_n = n;
+        return s;
     }
-}
-
-typedef struct {
-    int32_t id, prev, next;
-} Sym;
-
-static int cand_less(const Cand *a, const Cand *b) { return a->rank < b->rank || (a->rank == b->rank && a->pos < b->pos); }
-
-static int queue_pair(Tokenizer *t, const Sym *sy, int32_t p) {
-    const int32_t q = sy[p].next;
-    const int r = rank_of(t, sy[p].id, sy[q].id);
-    if (r < 0) return 0;
-    Grow *g = &t->queue;
-    if (grow(g, g->n + 1, sizeof(Cand))) return -1;
-    Cand *h = (Cand *)g->p, x = {(uint32_t)r, (uint32_t)p, sy[p].id, sy[q].id};
-    size_t i = g->n++;
-    while (i > 0 && cand_less(&x, &h[(i - 1) / 2])) { h[i] = h[(i - 1) / 2]; i = (i - 1) / 2; }
-    h[i] = x;
-    return 0;
-}
-
-static Cand queue_pop(Tokenizer *t) {
-    Grow *g = &t->queue;
-    Cand *h = (Cand *)g->p, top = h[0], x = h[--g->n];
-    size_t i = 0;
-    for (;;) {
-        size_t c = 2 * i + 1;
-        if (c >= g->n) break;
-        if (c + 1 < g->n && cand_less(&h[c + 1], &h[c])) c++;
-        if (!cand_less(&h[c], &x)) break;
-        h[i] = h[c];
-        i = c;
+    /* a canonical decomposition is at most 4 code points, and composition only shortens */
+    uint8_t *o = reserve(&t->norm, 16 * nu + 16);
+    Mark *m = reserve(&t->marks, (4 * nu + 4) * sizeof(Mark));
+    if (!o || !m) return NULL;
+    size_t on = 0;
+    for (size_t a = 0; a < nu;) {
+        /* quiet units that no following unit depends on are copied as they are */
+        size_t b = a;
+        while (b < nu && !is_dirty(&u[b]) && !(b + 1 < nu && is_dirty(&u[b + 1]))) b++;
+        const size_t from = u[a].off, to = b < nu ? u[b].off : n;
+        memcpy(o + on, s + from, to - from);
+        on += to - from;
+        if (b == nu) break;
+        /* a piece: its head (quiet, or the span's first unit) and the units up to the next quiet one */
+        size_t e = b + 1;
+        while (e < nu && is_dirty(&u[e])) e++;
+        on += nfc_piece(t, u + b, e - b, o + on, m);
+        a = e;
     }
-    if (g->n) h[i] = x;
-    return top;
+    *out_n = on;
+    return o;
 }
 
-/* appends the ids of the pre-token w[0..n) to ids; -1 when they do not fit or memory runs out */
-static int bpe(Tokenizer *t, const uint8_t *w, size_t n, int *ids, int *cnt, int max_ids) {
-    if (grow(&t->sym, n, sizeof(Sym))) return -1;
-    Sym *sy = (Sym *)t->sym.p;
-    const int32_t end = (int32_t)n;
-    for (int32_t i = 0; i < end; i++) sy[i] = (Sym){t->byte_tok[w[i]], i - 1, i + 1};
-    t->queue.n = 0;
-    for (int32_t i = 0; i + 1 < end; i++)
-        if (queue_pair(t, sy, i)) return -1;
-    while (t->queue.n) {
-        const Cand c = queue_pop(t);
-        const int32_t p = (int32_t)c.pos, q = sy[p].next;
-        if (sy[p].id != c.left || q >= end || sy[q].id != c.right) continue; /* merged away since queued */
-        sy[p].id = (int32_t)t->merges[3 * (size_t)c.rank + 2];
-        sy[q].id = -1;
-        sy[p].next = sy[q].next;
-        if (sy[q].next < end) sy[sy[q].next].prev = p;
-        if (sy[p].prev >= 0 && queue_pair(t, sy, sy[p].prev)) return -1;
-        if (sy[p].next < end && queue_pair(t, sy, p)) return -1;
-    }
-    for (int32_t i = 0; i < end; i = sy[i].next) {
-        if (*cnt >= max_ids) return -1;
-        ids[(*cnt)++] = sy[i].id;
+/* ---- pre-tokenizer: the alternatives of the Split regex, each the length of its match in units (0 = none) */
+
+typedef size_t (*Alternative)(const Unit *u, size_t i, size_t n);
+
+static size_t run_of(const Unit *u, size_t i, size_t n, unsigned cls) {
+    size_t j = i;
+    while (j < n && unit_class(&u[j]) == cls) j++;
+    return j - i;
+}
+
+/* (?i:'s|'t|'re|'ve|'m|'ll|'d): under Oniguruma's case folding the only other spelling is U+017F for s */
+static size_t alt_contraction(const Unit *u, size_t i, size_t n) {
+    static const char *const tails[] = {"s", "t", "re", "ve", "m", "ll", "d"};
+    if (u[i].cp != '\'') return 0;
+    for (size_t k = 0; k < sizeof tails / sizeof *tails; k++) {
+        const size_t len = strlen(tails[k]);
+        size_t j = 0;
+        for (; j < len && i + 1 + j < n; j++) {
+            const uint32_t c = u[i + 1 + j].cp, want = (uint32_t)tails[k][j];
+            if (c != want && c != want - 32 && !(want == 's' && c == 0x17F)) break;
+        }
+        if (j == len) return 1 + len;
     }
     return 0;
 }
 
-/* ------------------------------------------------------------------------------------------------------
- * encode / decode */
+/* [^\r\n\p{L}\p{N}]?\p{L}+ */
+static size_t alt_letters(const Unit *u, size_t i, size_t n) {
+    size_t lead = 0;
+    if (unit_class(&u[i]) != K_LETTER) {
+        if (unit_class(&u[i]) == K_NUMBER || is_crlf(u[i].cp)) return 0;
+        lead = 1;
+    }
+    const size_t m = run_of(u, i + lead, n, K_LETTER);
+    return m ? lead + m : 0;
+}
 
-static int encode_plain(Tokenizer *t, const uint8_t *s, size_t n, int *ids, int *cnt, int max_ids) {
-    s = normalize(t, s, n, &n);
-    if (!s) return -1;
-    for (size_t i = 0; i < n;) {
-        const size_t j = pretoken_end(t, s, i, n);
-        if (bpe(t, s + i, j - i, ids, cnt, max_ids)) return -1;
-        i = j;
+/* \p{N} */
+static size_t alt_number(const Unit *u, size_t i, size_t n) {
+    (void)n;
+    return unit_class(&u[i]) == K_NUMBER;
+}
+
+/*  ?[^\s\p{L}\p{N}]+[\r\n]* */
+static size_t alt_symbols(const Unit *u, size_t i, size_t n) {
+    size_t j = i + (u[i].cp == ' ');
+    const size_t m = run_of(u, j, n, K_OTHER);
+    if (!m) return 0; /* without the space the run would start on white space */
+    for (j += m; j < n && is_crlf(u[j].cp); j++) {
+    }
+    return j - i;
+}
+
+/* \s*[\r\n]+ : through the last CR / LF of the white-space run */
+static size_t alt_newlines(const Unit *u, size_t i, size_t n) {
+    const size_t m = run_of(u, i, n, K_SPACE);
+    size_t end = 0;
+    for (size_t k = 0; k < m; k++)
+        if (is_crlf(u[i + k].cp)) end = k + 1;
+    return end;
+}
+
+/* \s+(?!\S) : the run when it ends the text, else the run but its last unit */
+static size_t alt_trailing_space(const Unit *u, size_t i, size_t n) {
+    const size_t m = run_of(u, i, n, K_SPACE);
+    return i + m == n ? m : m ? m - 1 : 0;
+}
+
+/* \s+ */
+static size_t alt_space(const Unit *u, size_t i, size_t n) { return run_of(u, i, n, K_SPACE); }
+
+static const Alternative split_regex[] = {alt_contraction, alt_letters, alt_number, alt_symbols,
+                                          alt_newlines, alt_trailing_space, alt_space};
+
+static size_t pretoken(const Unit *u, size_t i, size_t n) {
+    for (size_t a = 0; a < sizeof split_regex / sizeof *split_regex; a++) {
+        const size_t m = split_regex[a](u, i, n);
+        if (m) return m;
+    }
+    return 1; /* every class has an alternative above; kept for safety */
+}
+
+/* ---- BPE -------------------------------------------------------------------------------------------------- */
+
+/* key of the pair that starts at slot i: rank << 32 | i (lowest rank, then leftmost), NO_PAIR without a merge */
+static uint64_t pair_key(const Tokenizer *t, int32_t a, int32_t b, size_t i) {
+    const int64_t r = map_get(&t->pair_rank, (uint64_t)(uint32_t)a << 32 | (uint32_t)b);
+    return r < 0 ? NO_PAIR : (uint64_t)r << 32 | i;
+}
+
+/* min-tree with `leaves` leaves in tr[leaves .. 2 leaves) */
+static void tree_set(uint64_t *tr, size_t leaves, size_t i, uint64_t key) {
+    size_t k = leaves + i;
+    tr[k] = key;
+    for (k >>= 1; k; k >>= 1) {
+        const uint64_t l = tr[2 * k], r = tr[2 * k + 1], v = l < r ? l : r;
+        if (tr[k] == v) break;
+        tr[k] = v;
+    }
+}
+
+/* BPE of the bytes w[0 .. n) (n >= 1): the ids in order into t->out; returns their count, -1 on no memory */
+static long bpe(Tokenizer *t, const uint8_t *w, size_t n) {
+    int32_t *out = reserve(&t->out, n * sizeof(int32_t));
+    if (!out) return -1;
+    if (n == 1) {
+        out[0] = t->byte_tok[w[0]];
+        return 1;
+    }
+    size_t leaves = 1;
+    while (leaves < n) leaves *= 2;
+    int32_t *sym = reserve(&t->sym, 3 * n * sizeof(int32_t));
+    uint64_t *tr = reserve(&t->tree, 2 * leaves * sizeof(uint64_t));
+    if (!sym || !tr) return -1;
+    int32_t *next = sym + n, *prev = sym + 2 * n; /* neighbours among the live slots (n / -1 at the ends) */
+    for (size_t i = 0; i < n; i++) {
+        sym[i] = t->byte_tok[w[i]];
+        next[i] = (int32_t)i + 1;
+        prev[i] = (int32_t)i - 1;
+    }
+    for (size_t i = 0; i < 2 * leaves; i++) tr[i] = NO_PAIR;
+    for (size_t i = 0; i + 1 < n; i++) tr[leaves + i] = pair_key(t, sym[i], sym[i + 1], i);
+    for (size_t k = leaves - 1; k; k--) tr[k] = tr[2 * k] < tr[2 * k + 1] ? tr[2 * k] : tr[2 * k + 1];
+    while (tr[1] != NO_PAIR) {
+        const size_t p = (uint32_t)tr[1], q = (size_t)next[p];
+        sym[p] = (int32_t)t->merges[3 * (tr[1] >> 32) + 2];
+        next[p] = next[q];
+        if ((size_t)next[q] < n) prev[next[q]] = (int32_t)p;
+        tree_set(tr, leaves, q, NO_PAIR);
+        tree_set(tr, leaves, p, (size_t)next[p] < n ? pair_key(t, sym[p], sym[next[p]], p) : NO_PAIR);
+        if (prev[p] >= 0) tree_set(tr, leaves, (size_t)prev[p], pair_key(t, sym[prev[p]], sym[p], (size_t)prev[p]));
+    }
+    long c = 0;
+    for (size_t i = 0; i < n; i = (size_t)next[i]) out[c++] = sym[i];
+    return c;
+}
+
+/* ---- encode / decode ------------------------------------------------------------------------------------- */
+
+/* ids of one span without added tokens, appended at ids[*count] */
+static int encode_span(Tokenizer *t, const uint8_t *s, size_t n, int *ids, int max_ids, int *count) {
+    if (!n) return 0;
+    size_t m, nu;
+    const uint8_t *x = nfc(t, s, n, &m);
+    if (!x) return -1;
+    const Unit *u = split_units(t, x, m, &nu);
+    if (!u) return -1;
+    for (size_t i = 0; i < nu;) {
+        const size_t k = pretoken(u, i, nu), from = u[i].off, to = i + k < nu ? u[i + k].off : m;
+        const long c = bpe(t, x + from, to - from);
+        if (c < 0 || c > (long)max_ids - *count) return -1;
+        memcpy(ids + *count, t->out.p, (size_t)c * sizeof(int));
+        *count += (int)c;
+        i += k;
     }
     return 0;
 }
@@ -431,155 +489,195 @@ static int encode_plain(Tokenizer *t, const uint8_t *s, size_t n, int *ids, int 
 int tok_encode(Tokenizer *t, const char *text, int allow_special, int *ids, int max_ids) {
     const uint8_t *s = (const uint8_t *)text;
     const size_t n = strlen(text);
-    int cnt = 0;
-    size_t from = 0;
-    for (size_t k = 0; k <= n; k++) {
-        const Special *best = NULL;
-        if (k < n && allow_special && t->spec_lead[s[k]])
+    int count = 0;
+    if (max_ids < 0) max_ids = 0;
+    for (size_t pos = 0;;) {
+        /* the next added token: leftmost start, longest text there */
+        size_t at = n;
+        int64_t hit = -1;
+        for (size_t k = pos; allow_special && hit < 0 && k < n; k++) {
+            if (!(t->lead[s[k] >> 3] >> (s[k] & 7) & 1)) continue;
             for (uint32_t a = 0; a < t->n_added; a++) {
-                const Special *x = &t->spec[a];
-                if (x->len <= n - k && !memcmp(s + k, x->text, x->len) && (!best || x->len > best->len)) best = x;
+                const uint32_t id = t->added_ids[a], len = t->piece_len[id];
+                if (len <= n - k && !memcmp(s + k, t->data + t->piece_at[id], len)) {
+                    hit = id;
+                    at = k;
+                    break;
+                }
             }
-        if (!best && k < n) continue;
-        if (encode_plain(t, s + from, k - from, ids, &cnt, max_ids)) return -1;
-        if (!best) break;
-        if (cnt >= max_ids) return -1;
-        ids[cnt++] = (int)best->id;
-        from = k + best->len;
-        k = from - 1;
+        }
+        if (encode_span(t, s + pos, at - pos, ids, max_ids, &count)) return -1;
+        if (hit < 0) return count;
+        if (count >= max_ids) return -1;
+        ids[count++] = (int)hit;
+        pos = at + t->piece_len[hit];
     }
-    return cnt;
 }
 
 const char *tok_decode(Tokenizer *t, int id, int *len) {
-    if (id >= 0 && (uint32_t)id < t->n_vocab) {
-        *len = t->tlen[id];
-        return (const char *)t->blob + t->toff[id];
-    }
-    for (uint32_t a = 0; a < t->n_added; a++)
-        if (t->spec[a].id == (uint32_t)id) {
-            *len = (int)t->spec[a].len;
-            return t->spec[a].text;
-        }
-    *len = 0;
-    return NULL;
+    const int known = id >= 0 && (uint32_t)id < t->n_ids && t->piece_len[id];
+    *len = known ? t->piece_len[id] : 0;
+    return known ? (const char *)t->data + t->piece_at[id] : NULL;
 }
 
 int tok_id(Tokenizer *t, const char *added_token) {
     const size_t n = strlen(added_token);
-    for (uint32_t a = 0; a < t->n_added; a++)
-        if (t->spec[a].len == n && !memcmp(t->spec[a].text, added_token, n)) return (int)t->spec[a].id;
+    for (uint32_t a = 0; a < t->n_added; a++) {
+        const uint32_t id = t->added_ids[a];
+        if (t->piece_len[id] == n && !memcmp(t->data + t->piece_at[id], added_token, n)) return (int)id;
+    }
     return -1;
 }
 
 int tok_vocab_size(Tokenizer *t) { return (int)t->n_ids; }
 
-/* ------------------------------------------------------------------------------------------------------
- * load */
+/* ---- load ----------------------------------------------------------------------------------------------------- */
 
 void tok_free(Tokenizer *t) {
     if (!t) return;
-    free(t->file);
-    free(t->toff);
-    free(t->mkey);
-    free(t->mval);
-    free(t->spec);
-    free(t->cps.p);
-    free(t->marks.p);
-    free(t->out.p);
-    free(t->sym.p);
-    free(t->queue.p);
+    map_free(&t->pair_rank);
+    map_free(&t->decomp);
+    map_free(&t->compose);
+    Scratch *s[] = {&t->norm, &t->units, &t->marks, &t->sym, &t->tree, &t->out};
+    for (size_t i = 0; i < sizeof s / sizeof *s; i++) free(s[i]->p);
+    free(t->piece_at);
+    free(t->piece_len);
+    free(t->added_ids);
+    free(t->data);
     free(t);
 }
 
 typedef struct {
-    const uint8_t *p, *end;
+    const uint8_t *at, *end;
 } Cursor;
 
-/* the next section of `bytes` bytes (then padding to 4), or NULL when the file is too short */
-static const void *take(Cursor *c, size_t bytes) {
-    const size_t padded = (bytes + 3) & ~(size_t)3;
-    if (padded < bytes || padded > (size_t)(c->end - c->p)) return NULL;
-    const void *r = c->p;
-    c->p += padded;
-    return r;
+/* the next section of `bytes` bytes (padded to 4), NULL past the end of the file */
+static const void *section(Cursor *c, uint64_t bytes) {
+    const uint64_t padded = (bytes + 3) & ~(uint64_t)3;
+    if (padded > (uint64_t)(c->end - c->at)) return NULL;
+    const void *p = c->at;
+    c->at += padded;
+    return p;
+}
+
+static uint8_t *read_file(const char *path, size_t *size) {
+    FILE *f = fopen(path, "rb");
+    if (!f) return NULL;
+    uint8_t *buf = NULL;
+    long n = -1;
+    if (!fseek(f, 0, SEEK_END)) n = ftell(f);
+    if (n > 0 && !fseek(f, 0, SEEK_SET) && (buf = malloc((size_t)n)) && fread(buf, 1, (size_t)n, f) == (size_t)n) {
+        *size = (size_t)n;
+    } else {
+        free(buf);
+        buf = NULL;
+    }
+    fclose(f);
+    return buf;
+}
+
+/* parses the file held in t->data; returns NULL or what is wrong with it */
+static const char *parse(Tokenizer *t, size_t size) {
+    Cursor c = {t->data, t->data + size};
+    const char *magic = section(&c, 8);
+    const uint32_t *h = section(&c, 48);
+    if (!magic || !h || memcmp(magic, "QWTOK001", 8)) return "not a QWTOK001 file";
+    const uint32_t n_vocab = h[0], n_added = h[1], n_merges = h[2], blob_len = h[3], n_runs = h[4], n_dec = h[5],
+                   pool_len = h[6], n_comp = h[7];
+    if (n_vocab < 256 || n_vocab > (1u << 20) || n_added > 4096 || n_runs == 0) return "bad header";
+    const uint8_t *len = section(&c, n_vocab), *blob = section(&c, blob_len);
+    t->merges = section(&c, 12ull * n_merges);
+    if (!len || !blob || !t->merges) return "file too short";
+    t->n_base = n_vocab;
+    t->n_added = n_added;
+    /* ids: the base vocabulary, then the added tokens (their ids given in the file) */
+    const uint32_t **added = calloc(n_added + 1, sizeof *added);
+    if (!added) return "out of memory";
+    uint32_t n_ids = n_vocab;
+    const char *why = NULL;
+    for (uint32_t a = 0; a < n_added && !why; a++) {
+        const uint32_t *e = section(&c, 8);
+        if (!e || !section(&c, e[1])) why = "file too short";
+        else if (e[0] < n_vocab || e[0] >= (1u << 20) || e[1] == 0 || e[1] > 0xFFFF) why = "bad added token";
+        else {
+            added[a] = e;
+            if (e[0] + 1 > n_ids) n_ids = e[0] + 1;
+        }
+    }
+    t->runs = why ? NULL : section(&c, 4ull * n_runs);
+    const uint32_t *dec_cp = section(&c, 4ull * n_dec);
+    t->dec_off = section(&c, 4ull * n_dec + 4);
+    t->dec_pool = section(&c, 4ull * pool_len);
+    const uint32_t *comp = section(&c, 12ull * n_comp);
+    if (!why && (!t->runs || !dec_cp || !t->dec_off || !t->dec_pool || !comp)) why = "file too short";
+    if (!why && (t->runs[0] & 0x1FFFFF)) why = "bad Unicode table";
+    for (uint32_t i = 0; !why && i < n_dec; i++)
+        if (t->dec_off[i] > t->dec_off[i + 1] || t->dec_off[i + 1] > pool_len || t->dec_off[i + 1] - t->dec_off[i] > 4)
+            why = "bad decomposition table";
+    t->n_ids = n_ids;
+    t->piece_at = calloc(n_ids, sizeof *t->piece_at);
+    t->piece_len = calloc(n_ids, sizeof *t->piece_len);
+    t->added_ids = calloc(n_added + 1, sizeof *t->added_ids);
+    if (!why && (!t->piece_at || !t->piece_len || !t->added_ids)) why = "out of memory";
+    if (why) {
+        free(added);
+        return why;
+    }
+    uint64_t off = (uint64_t)(blob - t->data);
+    for (uint32_t i = 0; i < n_vocab; i++) {
+        t->piece_at[i] = (uint32_t)off;
+        t->piece_len[i] = len[i];
+        off += len[i];
+        if (!len[i]) why = "empty token";
+    }
+    if (off != (uint64_t)(blob - t->data) + blob_len) why = "token lengths do not add up to the blob";
+    for (uint32_t a = 0; a < n_added; a++) {
+        const uint32_t id = added[a][0];
+        if (t->piece_len[id]) why = "an id twice";
+        t->piece_at[id] = (uint32_t)((const uint8_t *)(added[a] + 2) - t->data);
+        t->piece_len[id] = (uint16_t)added[a][1];
+        t->added_ids[a] = id;
+        const uint8_t b = ((const uint8_t *)(added[a] + 2))[0];
+        t->lead[b >> 3] |= (uint8_t)(1u << (b & 7));
+    }
+    free(added);
+    /* longest added token first (the match taken at a position), ties by id */
+    for (uint32_t a = 1; a < n_added; a++) {
+        const uint32_t id = t->added_ids[a];
+        uint32_t b = a;
+        for (; b > 0 && t->piece_len[t->added_ids[b - 1]] < t->piece_len[id]; b--) t->added_ids[b] = t->added_ids[b - 1];
+        t->added_ids[b] = id;
+    }
+    for (int b = 0; b < 256; b++) t->byte_tok[b] = -1;
+    for (uint32_t i = 0; i < n_vocab; i++)
+        if (len[i] == 1) t->byte_tok[t->data[t->piece_at[i]]] = (int32_t)i;
+    for (int b = 0; b < 256; b++)
+        if (t->byte_tok[b] < 0) why = "a single-byte token is missing";
+    if (why) return why;
+    t->n_runs = n_runs;
+    for (uint32_t cp = 0; cp < 256; cp++) t->low_pay[cp] = (uint16_t)run_payload(t, cp);
+    if (map_init(&t->pair_rank, n_merges) || map_init(&t->decomp, n_dec) || map_init(&t->compose, n_comp))
+        return "out of memory";
+    for (uint32_t r = 0; r < n_merges; r++) {
+        const uint32_t *m = t->merges + 3 * r;
+        if (m[0] >= n_vocab || m[1] >= n_vocab || m[2] >= n_vocab) return "merge with an unknown id";
+        map_put(&t->pair_rank, (uint64_t)m[0] << 32 | m[1], r);
+    }
+    for (uint32_t i = 0; i < n_dec; i++) map_put(&t->decomp, dec_cp[i], i);
+    for (uint32_t i = 0; i < n_comp; i++) map_put(&t->compose, (uint64_t)comp[3 * i] << 32 | comp[3 * i + 1], comp[3 * i + 2]);
+    return NULL;
 }
 
 Tokenizer *tok_load(const char *path) {
-    Tokenizer *t = (Tokenizer *)calloc(1, sizeof *t);
+    Tokenizer *t = calloc(1, sizeof *t);
+    size_t size = 0;
     const char *why = "out of memory";
-    FILE *f = NULL;
-    if (!t) goto fail;
-    why = "cannot read the file";
-    if (!(f = fopen(path, "rb")) || fseek(f, 0, SEEK_END)) goto fail;
-    const long size = ftell(f);
-    if (size < 56 || fseek(f, 0, SEEK_SET)) goto fail;
-    if (!(t->file = (uint8_t *)malloc((size_t)size)) || fread(t->file, 1, (size_t)size, f) != (size_t)size) goto fail;
-    fclose(f);
-    f = NULL;
-    why = "not a QWTOK001 tokenizer file, or a damaged one";
-    if (memcmp(t->file, "QWTOK001", 8)) goto fail;
-    uint32_t h[12];
-    memcpy(h, t->file + 8, sizeof h);
-    t->n_vocab = h[0]; t->n_added = h[1]; t->n_merges = h[2]; t->n_uni = h[4]; t->n_dec = h[5]; t->pool_len = h[6];
-    t->n_comp = h[7];
-    if (t->n_vocab < 256 || t->n_vocab > (1u << 24) || t->n_merges > (1u << 24) || t->n_uni == 0 ||
-        t->n_added > (1u << 16))
-        goto fail;
-    Cursor c = {t->file + 56, t->file + size};
-    if (!(t->tlen = (const uint8_t *)take(&c, t->n_vocab)) || !(t->blob = (const uint8_t *)take(&c, h[3])) ||
-        !(t->merges = (const uint32_t *)take(&c, (size_t)t->n_merges * 12)))
-        goto fail;
-    if (!(t->spec = (Special *)calloc(t->n_added + 1, sizeof(Special)))) goto fail;
-    t->n_ids = t->n_vocab;
-    for (uint32_t a = 0; a < t->n_added; a++) {
-        const uint32_t *e = (const uint32_t *)take(&c, 8);
-        if (!e || e[1] == 0 || !(t->spec[a].text = (const char *)take(&c, e[1]))) goto fail;
-        t->spec[a].id = e[0];
-        t->spec[a].len = e[1];
-        t->spec_lead[(uint8_t)t->spec[a].text[0]] = 1;
-        if (e[0] >= t->n_ids) t->n_ids = e[0] + 1;
+    if (t) {
+        t->data = read_file(path, &size);
+        why = !t->data ? "cannot read the file" : size > 0xFFFFFFF0u ? "file too large" : parse(t, size);
     }
-    if (!(t->uni = (const uint32_t *)take(&c, (size_t)t->n_uni * 4)) ||
-        !(t->dec_cp = (const uint32_t *)take(&c, (size_t)t->n_dec * 4)) ||
-        !(t->dec_off = (const uint32_t *)take(&c, ((size_t)t->n_dec + 1) * 4)) ||
-        !(t->dec_pool = (const uint32_t *)take(&c, (size_t)t->pool_len * 4)) ||
-        !(t->comp = (const uint32_t *)take(&c, (size_t)t->n_comp * 12)))
-        goto fail;
-    for (uint32_t i = 0; i < t->n_dec; i++)
-        if (t->dec_off[i] > t->dec_off[i + 1] || t->dec_off[i + 1] > t->pool_len) goto fail;
-    /* token offsets; every byte needs a one-byte token */
-    if (!(t->toff = (uint32_t *)malloc(((size_t)t->n_vocab + 1) * 4))) goto fail;
-    uint64_t off = 0;
-    for (uint32_t i = 0; i < t->n_vocab; i++) { t->toff[i] = (uint32_t)off; off += t->tlen[i]; }
-    if (off != h[3]) goto fail;
-    t->toff[t->n_vocab] = (uint32_t)off;
-    for (int b = 0; b < 256; b++) t->byte_tok[b] = -1;
-    for (uint32_t i = 0; i < t->n_vocab; i++)
-        if (t->tlen[i] == 1 && t->byte_tok[t->blob[t->toff[i]]] < 0) t->byte_tok[t->blob[t->toff[i]]] = (int32_t)i;
-    for (int b = 0; b < 256; b++)
-        if (t->byte_tok[b] < 0) goto fail;
-    /* merge table, load factor <= 1/2 */
-    uint32_t slots = 1024;
-    while (slots < 2 * t->n_merges) slots *= 2;
-    t->mmask = slots - 1;
-    if (!(t->mkey = (uint64_t *)calloc(slots, 8)) || !(t->mval = (uint32_t *)malloc((size_t)slots * 4))) goto fail;
-    for (uint32_t r = 0; r < t->n_merges; r++) {
-        const uint32_t *m = t->merges + 3 * (size_t)r;
-        if (m[0] >= t->n_vocab || m[1] >= t->n_vocab || m[2] >= t->n_vocab) goto fail;
-        const uint64_t key = pair_key(m[0], m[1]) + 1;
-        uint32_t s = slot_of(key, t->mmask);
-        while (t->mkey[s] && t->mkey[s] != key) s = (s + 1) & t->mmask;
-        if (t->mkey[s]) continue; /* a repeated pair keeps its first (lowest) rank */
-        t->mkey[s] = key;
-        t->mval[s] = r;
-    }
-    t->hit_lo = t->hit_hi = 0;
-    for (uint32_t cp = 0; cp < 128; cp++) t->ascii_cls[cp] = (uint8_t)(payload(t, cp) & 3);
-    return t;
-fail:
-    fprintf(stderr, "tok_load(%s): %s\n", path, why);
-    if (f) fclose(f);
+    if (!why) return t;
+    fprintf(stderr, "qwen tokenizer %s: %s\n", path, why);
     tok_free(t);
     return NULL;
 }
