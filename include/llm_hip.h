@@ -14,10 +14,9 @@
  *     layer output matches the reference within fp32 rounding (an int8 re-quantization that lands on the
  *     other side of a rounding boundary then moves deeper layers by more; see llm_set_strict);
  *   strict (LLM_STRICT=1 at llm_open, or llm_set_strict): every float operation of forward() in the
- *     reference's order and the reference libm's expf, so logits and greedy token streams are bitwise those of
- *     qwen.c / runq.c built with strict IEEE flags (the device sampler's softmax and cdf are tree sums in both
- *     modes: sampled streams follow the reference's draws only where no probability lies within rounding of a
- *     cut).  llama2.c .bin GEMVs always sum their groups in order.
+ *     reference's order and the reference libm's expf, so logits and token streams, greedy or sampled (the
+ *     sampler's softmax and cumulative sums sequential as the reference's), are bitwise those of qwen.c /
+ *     runq.c built with strict IEEE flags.  llama2.c .bin GEMVs always sum their groups in order.
  * Errors: -1 (or NULL) with a message on stderr, the reference's convention (matvec_fpga.h:15). */
 #pragma once
 #include <stddef.h>
@@ -146,6 +145,15 @@ int mvh_group_dots(const uint8_t *w, const int8_t *xq, int n, int d, int bits, i
  * state (*rng in, the advanced state out), temperature > 0; rows[count] receives the sampled rows */
 int mvh_sample(const float *logits, int n, int count, float temperature, float topp, unsigned long long *rng,
                int *rows);
+/* the same with the strict mode's draw: every float operation of the reference's sample() in its order
+ * (sequential softmax sum and cumulative sums, candidates in qsort's order), so rows and RNG state are those of
+ * the reference's sampler for any logits; n <= 262144 */
+int mvh_sample_strict(const float *logits, int n, int count, float temperature, float topp,
+                      unsigned long long *rng, int *rows);
+/* mvh_sample_strict with every predicted segment start of its sequential sums moved by `skew` ulps: from 32 on,
+ * no start is among its segment's candidates and every sum takes the term-by-term path (its tests) */
+int mvh_sample_strict_skew(const float *logits, int n, int count, float temperature, float topp,
+                           unsigned long long *rng, int *rows, int skew);
 /* the prefill GEMM on caller data: y[m][r] for M tokens, weights in the reference layout (qwen planes: bits 4
  * or 8 with fp16 scales, group 32; runq: bits 0 = int8 with fp32 scales, group gs), tiled with row-blocks of
  * rb (8, 16 or 64) rows; xq [M][n] int8, xs [M][n/gs], y [M][d].  shape: 0 the library's choice, 10 TA + TB

@@ -85,6 +85,8 @@ def lib():
     L.llm_sampler_state.argtypes = [vp, C.POINTER(C.c_ulonglong)]
     L.mvh_sample.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
     L.mvh_sample_noalloc.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
+    L.mvh_sample_strict.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
+    L.mvh_sample_strict_skew.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp, i32]
     L.mvh_ref_expf.argtypes = [vp, i32, vp]
     L.mvh_ref_expf_host.argtypes = [vp, i32, vp]
     L.llm_set_strict.argtypes = [vp, i32]
@@ -133,15 +135,21 @@ def prefill_gemm(w, ws, xq, xs, M, n, d, bits, gs=32, rb=16, shape=0):
     return y
 
 
-def sample(logits, temperature, topp, seed, noalloc=False):
+def sample(logits, temperature, topp, seed, noalloc=False, strict=False, skew=None):
     """The on-device sampler on caller logits [count, n] (or [n]), drawn in order with one RNG state seeded by
-    `seed`: (rows, the advanced RNG state).  noalloc: the entry point that allocates no device memory."""
+    `seed`: (rows, the advanced RNG state).  noalloc: the entry point that allocates no device memory; strict:
+    the strict mode's draw (the reference's sample() operation for operation); skew: the strict draw with its
+    segment predictions moved by that many ulps (its term-by-term path)."""
     lg = np.ascontiguousarray(np.atleast_2d(logits), dtype=np.float32)
     rows = np.empty(lg.shape[0], np.int32)
     st = C.c_ulonglong(seed)
-    fn = lib().mvh_sample_noalloc if noalloc else lib().mvh_sample
-    if fn(_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)) != 0:
-        raise RuntimeError("mvh_sample_noalloc failed" if noalloc else "mvh_sample failed")
+    args = [_ptr(lg), lg.shape[1], lg.shape[0], temperature, topp, C.byref(st), _ptr(rows)]
+    if skew is not None:
+        name, args = "mvh_sample_strict_skew", args + [skew]
+    else:
+        name = "mvh_sample_strict" if strict else "mvh_sample_noalloc" if noalloc else "mvh_sample"
+    if getattr(lib(), name)(*args) != 0:
+        raise RuntimeError(name + " failed")
     return rows, st.value
 
 

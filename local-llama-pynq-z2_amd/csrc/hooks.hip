@@ -163,17 +163,17 @@ extern "C" int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *
     return rc;
 }
 
-extern "C" int mvh_sample(const float *logits, int n, int count, float temperature, float topp,
-                          unsigned long long *rng, int *rows) {
+static int sample_hook(const char *who, int strict, const float *logits, int n, int count, float temperature,
+                       float topp, unsigned long long *rng, int *rows, int skew = 0) {
     if (!logits || !rng || !rows || n < 2 || count < 1 || !(temperature > 0.0f)) {
-        fprintf(stderr, "mvh_sample: bad arguments (n=%d count=%d temperature=%g)\n", n, count, temperature);
+        fprintf(stderr, "%s: bad arguments (n=%d count=%d temperature=%g)\n", who, n, count, temperature);
         return -1;
     }
-    if (hook_device("mvh_sample")) return -1;
+    if (hook_device(who)) return -1;
     float *dl = nullptr, *dp = nullptr;
     int *dr = nullptr;
     SamplerState *dss = nullptr;
-    void *dsc = nullptr; // the many-workgroup draw's buffers (taken for large n)
+    void *dsc = nullptr; // the many-workgroup draw's buffers (taken for large n), or the strict draw's
     SamplerState st;
     st.temperature = temperature;
     st.topp = topp;
@@ -182,9 +182,10 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     const size_t ld = ((size_t)n + 3) & ~(size_t)3; // 16-byte aligned rows
     if (hipMalloc(&dl, (size_t)count * ld * 4) == hipSuccess && hipMalloc(&dp, (size_t)n * 4) == hipSuccess &&
         hipMalloc(&dr, (size_t)count * 4) == hipSuccess && hipMalloc(&dss, sizeof st) == hipSuccess &&
-        hipMalloc(&dsc, sample_scratch_bytes()) == hipSuccess &&
+        hipMalloc(&dsc, strict ? sample_strict_scratch_bytes() : sample_scratch_bytes()) == hipSuccess &&
         hipMemcpy2D(dl, ld * 4, logits, (size_t)n * 4, (size_t)n * 4, count, hipMemcpyHostToDevice) == hipSuccess &&
-        hipMemcpy(dss, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess) {
+        hipMemcpy(dss, &st, sizeof st, hipMemcpyHostToDevice) == hipSuccess &&
+        (!strict || sample_strict_set_skew(dsc, skew) == hipSuccess)) {
         rc = 0;
         for (int c = 0; c < count && !rc; c++) {
             SampleArgs a;
@@ -194,7 +195,9 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
             a.probs = dp;
             a.ss = dss;
             a.out_row = dr + c;
-            a.scratch = dsc;
+            a.scratch = strict ? nullptr : dsc;
+            a.strict = strict;
+            a.strict_scratch = strict ? dsc : nullptr;
             a.path = topp > 0.0f && topp < 1.0f ? 1 : 0;
             if (launch_sample(a, 0) != hipSuccess) rc = -1;
         }
@@ -203,7 +206,7 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
                     hipMemcpy(&st, dss, sizeof st, hipMemcpyDeviceToHost) != hipSuccess))
             rc = -1;
     }
-    if (rc) fprintf(stderr, "mvh_sample: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    if (rc) fprintf(stderr, "%s: HIP error %s\n", who, hipGetErrorString(hipGetLastError()));
     else *rng = st.rng;
     hipFree(dl);
     hipFree(dp);
@@ -211,6 +214,21 @@ extern "C" int mvh_sample(const float *logits, int n, int count, float temperatu
     hipFree(dss);
     hipFree(dsc);
     return rc;
+}
+
+extern "C" int mvh_sample(const float *logits, int n, int count, float temperature, float topp,
+                          unsigned long long *rng, int *rows) {
+    return sample_hook("mvh_sample", 0, logits, n, count, temperature, topp, rng, rows);
+}
+
+extern "C" int mvh_sample_strict(const float *logits, int n, int count, float temperature, float topp,
+                                 unsigned long long *rng, int *rows) {
+    return sample_hook("mvh_sample_strict", 1, logits, n, count, temperature, topp, rng, rows);
+}
+
+extern "C" int mvh_sample_strict_skew(const float *logits, int n, int count, float temperature, float topp,
+                                      unsigned long long *rng, int *rows, int skew) {
+    return sample_hook("mvh_sample_strict_skew", 1, logits, n, count, temperature, topp, rng, rows, skew);
 }
 
 // ref_expf (the reference libm's expf, used by the strict mode) over caller data, on the device and, with the

@@ -132,9 +132,16 @@ struct SampleArgs {
     void *scratch;
     int path;               // many-workgroup path: the kernels launched, 0 the plain walk, 1 top-p, else both
                             // (each returns at once unless the device-resident settings select it)
+    // strict mode: the reference-order draw (sample_strict.hip) with its buffers (sample_strict_scratch_bytes())
+    int strict;
+    void *strict_scratch;
 };
 hipError_t launch_sample(const SampleArgs &a, hipStream_t st);
 size_t sample_scratch_bytes();
+hipError_t launch_sample_strict(const SampleArgs &a, hipStream_t st);
+size_t sample_strict_scratch_bytes();
+// tests: move every predicted segment start of the strict draw's sums by `skew` ulps (0 after allocation)
+hipError_t sample_strict_set_skew(void *scratch, int skew);
 
 struct RepackArgs {
     TiledMat T;             // output (T.data writable)

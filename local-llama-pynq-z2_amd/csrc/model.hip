@@ -90,6 +90,7 @@ struct llm_model {
     SamplerState *ss = nullptr;
     float *smp_p = nullptr;
     void *smp_scratch = nullptr; // the many-workgroup draw's buffers (large vocabularies)
+    void *smp_strict = nullptr;  // the reference-order draw's buffers (strict mode)
     int smp_path = -1;           // top-p (1) or the plain walk (0): the sampled step graphs launch that path only
     hipGraphExec_t g_plain_s = nullptr, g_hist_s = nullptr;
     // prefill: activation matrices of up to pf_cap tokens (allocated on first use)
@@ -210,6 +211,8 @@ hipError_t launch_sampler(llm_model *m) {
     a.np = m->s_head.grid;
     a.scratch = m->smp_scratch;
     a.path = m->smp_path;
+    a.strict = m->strict;
+    a.strict_scratch = m->smp_strict;
     return launch_sample(a, m->st);
 }
 
@@ -1389,7 +1392,8 @@ extern "C" int llm_set_sampler(llm_model *m, float temperature, float topp, unsi
     HIP_OR_FAIL("llm_set_sampler", hipStreamSynchronize(m->st));
     const size_t n = (size_t)m->info.n_logits;
     if (!m->ss && (dalloc(m, &m->ss, sizeof(SamplerState)) || dalloc(m, &m->smp_p, n * 4) ||
-                   dalloc(m, (uint8_t **)&m->smp_scratch, sample_scratch_bytes())))
+                   dalloc(m, (uint8_t **)&m->smp_scratch, sample_scratch_bytes()) ||
+                   dalloc(m, (uint8_t **)&m->smp_strict, sample_strict_scratch_bytes())))
         return -1;
     SamplerState st;
     st.temperature = temperature;

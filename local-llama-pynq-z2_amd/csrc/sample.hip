@@ -869,6 +869,7 @@ __global__ void __launch_bounds__(SMB_T) ks_final(SampleArgs a, int sel) {
 size_t sample_scratch_bytes() { return sizeof(SmpScratch); }
 
 hipError_t launch_sample(const SampleArgs &a, hipStream_t st) {
+    if (a.strict) return launch_sample_strict(a, st);
     if (a.n < 2 || a.n > SMP_MAX_CHUNKS * SMP_CHUNK || !a.logits || !a.probs || !a.ss ||
         ((uintptr_t)a.logits & 15) || ((uintptr_t)a.probs & 15) || (a.np > 0 && (!a.pv || !a.pi)))
         return hipErrorInvalidValue;
