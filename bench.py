@@ -14,6 +14,7 @@ the fast mode (tree sums) is timed too and reported as the sub-record "fast".  -
                   [--no-c5] [--no-c4] [--fast] [--single-mode]
   python bench.py --traffic-from D --traffic-all     (every kernel kind's HBM bytes per launch from the passes in D)
   python bench.py --trace-summary T.csv              (a rocprofv3 kernel trace grouped by kernel and grid)
+  python bench.py --floor                            (a plain streaming read of each layer GEMV's bytes per launch)
   The default run (c3) also measures the Qwen2-7B shape (c5) and the 512-token batched prefill of its own model
   (c4), and reports them as the sub-records "c5" and "c4".
   roofline.traffic (HBM bytes per launch of the dominant kernel) comes from two rocprofv3 --pmc passes that the
@@ -544,6 +545,41 @@ def measure(a, name, steps, warmup, profile_steps, cpu_tokens, counters, baselin
     return out
 
 
+FLOOR_SHAPES = {  # (dim, hidden, kv_dim, layers) of the Qwen2 shapes; every layer matrix Q4_0 (fp16 scales, groups of 32)
+    "c3": (896, 4864, 128, 24),
+    "c5": (3584, 18944, 512, 28),
+}
+
+
+def gemv_bytes(d, n, wbits=4, gs=32, s=2):
+    """algorithmic bytes of one GEMV launch: weights, scales, int8 input and its scales, fp32 output"""
+    return d * n * wbits // 8 + d * (n // gs) * s + n + (n // gs) * 4 + d * 4
+
+
+def read_floor(a):
+    """the floor of one launch: a plain streaming read of each layer GEMV's algorithmic bytes, one launch per
+    layer over distinct buffers in a graph (so no launch finds its bytes in a cache), non-temporal loads as the
+    decode GEMVs use at these sizes, over several grid sizes; against the GEMVs' in-graph times of a bench run"""
+    P = load_pkg()
+    out = {"metric": "plain-read floor per launch (us, GB/s, fraction of 8 TB/s)", "shapes": {}}
+    for name, (dim, hid, kv, layers) in FLOOR_SHAPES.items():
+        kinds = {"qkv_gemv": gemv_bytes(dim + 2 * kv, dim), "o_gemv": gemv_bytes(dim, dim),
+                 "gateup_gemv": gemv_bytes(2 * hid, dim), "down_gemv": gemv_bytes(dim, hid)}
+        rec = {}
+        for kind, nbytes in kinds.items():
+            grid = {}
+            for blocks in (256, 512, 1024, 2048):
+                us = P.read_floor(nbytes, layers, blocks, nt=True, reps=20)
+                grid[blocks] = round(us, 3)
+            best = min(grid.values())
+            rec[kind] = {"bytes": nbytes, "us": best, "GB_s": round(nbytes / best / 1e3, 1),
+                         "frac": round(nbytes / best / 1e3 / 8000.0, 4), "us_by_blocks": grid}
+            log(f"[floor {name}] {kind:12s} {nbytes / 1e6:8.3f} MB: {best:7.2f} us per launch, "
+                f"{nbytes / best / 1e3:7.1f} GB/s ({nbytes / best / 1e3 / 80:.1f}% of 8 TB/s); by blocks {grid}")
+        out["shapes"][name] = rec
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -571,6 +607,8 @@ def main():
     ap.add_argument("--traffic-from", default=None, help="directory with the FETCH_SIZE/WRITE_SIZE passes")
     ap.add_argument("--traffic-all", action="store_true",
                     help="with --traffic-from: print every kernel kind's HBM bytes per launch and stop")
+    ap.add_argument("--floor", action="store_true",
+                    help="the plain-read floor of each layer GEMV's bytes per launch (C3 and C5 shapes), and stop")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print a rocprofv3 kernel trace grouped by kernel and grid, and stop")
     a = ap.parse_args()
@@ -593,6 +631,8 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.init()
+    if a.floor:
+        return read_floor(a)
     if a.calib or a.counters:
         calib_copy()
     if a.counters:

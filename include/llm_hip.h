@@ -160,6 +160,10 @@ int mvh_sample_strict_skew(const float *logits, int n, int count, float temperat
  * one wave per 16 TA rows x 16 TB tokens: 11, 12, 14, 21, 22, 24, 41 or 42 */
 int mvh_prefill_gemm(const uint8_t *w, const void *ws, const int8_t *xq, const float *xs, int M, int n, int d,
                      int bits, int gs, int rb, int shape, float *y);
+/* the floor of a kernel that reads `bytes` once: `copies` launches of a plain streaming read (`blocks`
+ * workgroups, 8 loads of 16 bytes in flight per thread, non-temporal loads when nt != 0) over distinct buffers,
+ * captured as one graph and replayed `reps` times; *us gets the mean time per launch */
+int mvh_read_floor(size_t bytes, int copies, int blocks, int nt, int reps, float *us);
 /* the GEMV launch shape the library picks for a matrix, on the host (no device needed): rows x n weights in
  * groups of gs, wbits 4 or 8, scales fp32 (sf32 1) or fp16, row-blocks of rb rows, role 0 QKV, 1 attention output, 2 gate/up, 3 down,
  * 4 the output head's argmax, 5 a drop-in GEMV; ordered: bit 0 groups added in order, bit 1 the strict

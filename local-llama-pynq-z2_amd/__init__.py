@@ -88,6 +88,7 @@ def lib():
     L.mvh_sample_strict.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp]
     L.mvh_sample_strict_skew.argtypes = [vp, i32, i32, C.c_float, C.c_float, C.POINTER(C.c_ulonglong), vp, i32]
     L.mvh_ref_expf.argtypes = [vp, i32, vp]
+    L.mvh_read_floor.argtypes = [C.c_size_t, i32, i32, i32, i32, C.POINTER(C.c_float)]
     L.mvh_ref_expf_host.argtypes = [vp, i32, vp]
     L.llm_set_strict.argtypes = [vp, i32]
     L.llm_get_strict.argtypes = [vp]
@@ -151,6 +152,14 @@ def sample(logits, temperature, topp, seed, noalloc=False, strict=False, skew=No
     if getattr(lib(), name)(*args) != 0:
         raise RuntimeError(name + " failed")
     return rows, st.value
+
+
+def read_floor(nbytes, copies, blocks, nt=True, reps=20):
+    """µs per launch of a plain streaming read of nbytes (one launch per distinct buffer, in a graph)"""
+    us = C.c_float(0)
+    if lib().mvh_read_floor(nbytes, copies, blocks, int(nt), reps, C.byref(us)) != 0:
+        raise RuntimeError("mvh_read_floor failed")
+    return us.value
 
 
 def ref_expf(x, host=False):

@@ -282,3 +282,74 @@ extern "C" int mvh_gemv_shape(int rows, int n, int gs, int wbits, int sf32, int 
     out[3] = s.ord;
     return s.grid < 1 ? 1 : 0;
 }
+
+// A plain streaming read: block b reads its contiguous share of the buffer in 16-byte vectors, 8 in flight per
+// thread, with the weight loads' cache policy (0, or 2 = non-temporal), and keeps one word per block so that
+// no load is dead.  The floor of any kernel that must read those bytes once.
+template <int POLICY>
+__global__ void __launch_bounds__(256) k_read_floor(const uint8_t *p, uint32_t bytes, uint32_t *out) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, (int)bytes, 0x00020000);
+    const uint32_t vecs = bytes / 16, per = (vecs + gridDim.x - 1) / gridDim.x;
+    const uint32_t v0 = blockIdx.x * per, v1 = min(v0 + per, vecs);
+    uint32_t acc = 0;
+    for (uint32_t v = v0 + threadIdx.x; v < v1; v += 8 * 256) {
+        uint4 x[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t i = v + u * 256;
+            const auto r = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(i < v1 ? i * 16 : 0x80000000u), 0, POLICY);
+            x[u] = *(const uint4 *)&r;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc ^= x[u].x ^ x[u].y ^ x[u].z ^ x[u].w;
+    }
+    for (int o = 1; o < 64; o <<= 1) acc ^= __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) atomicXor(&out[blockIdx.x], acc);
+}
+
+extern "C" int mvh_read_floor(size_t bytes, int copies, int blocks, int nt, int reps, float *us) {
+    if (!us || bytes < 16 || bytes > 0x7fff0000u || copies < 1 || copies > 64 || blocks < 1 || blocks > 65536 ||
+        reps < 1 || (size_t)copies * ((bytes + 255) & ~(size_t)255) > ((size_t)8 << 30)) {
+        fprintf(stderr, "mvh_read_floor: bad arguments\n");
+        return -1;
+    }
+    if (hook_device("mvh_read_floor")) return -1;
+    const size_t stride = (bytes + 255) & ~(size_t)255;
+    uint8_t *buf = nullptr;
+    uint32_t *out = nullptr;
+    hipStream_t st = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = -1;
+    if (hipMalloc(&buf, (size_t)copies * stride) == hipSuccess && hipMalloc(&out, (size_t)blocks * 4) == hipSuccess &&
+        hipMemset(buf, 0x5a, (size_t)copies * stride) == hipSuccess && hipMemset(out, 0, (size_t)blocks * 4) == hipSuccess &&
+        hipStreamCreate(&st) == hipSuccess && hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+        hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) == hipSuccess) {
+        for (int c = 0; c < copies; c++) {
+            if (nt) hipLaunchKernelGGL(k_read_floor<2>, dim3(blocks), dim3(256), 0, st, buf + c * stride, (uint32_t)bytes, out);
+            else hipLaunchKernelGGL(k_read_floor<0>, dim3(blocks), dim3(256), 0, st, buf + c * stride, (uint32_t)bytes, out);
+        }
+        if (hipStreamEndCapture(st, &g) == hipSuccess && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess &&
+            hipGraphLaunch(ge, st) == hipSuccess && hipGraphLaunch(ge, st) == hipSuccess &&
+            hipEventRecord(e0, st) == hipSuccess) {
+            bool ok = true;
+            for (int r = 0; r < reps && ok; r++) ok = hipGraphLaunch(ge, st) == hipSuccess;
+            float ms = 0.0f;
+            if (ok && hipEventRecord(e1, st) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                hipEventElapsedTime(&ms, e0, e1) == hipSuccess) {
+                *us = ms * 1000.0f / (float)(reps * copies);
+                rc = 0;
+            }
+        }
+    }
+    if (rc) fprintf(stderr, "mvh_read_floor: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    if (ge) hipGraphExecDestroy(ge);
+    if (g) hipGraphDestroy(g);
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (st) hipStreamDestroy(st);
+    hipFree(buf);
+    hipFree(out);
+    return rc;
+}
