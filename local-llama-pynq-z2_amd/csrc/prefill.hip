@@ -1188,6 +1188,178 @@ __global__ void __launch_bounds__(256) k_p_attn_strict(ProwArgs a) {
                      a.p0 + m + 1, sm, a.xb + (size_t)m * a.dim + (size_t)h * hs);
 }
 
+// Strict prefill attention over tiles of tokens (qwen.c:526-546 for each token and head, in the reference's
+// order): block = (kv head, G consecutive tokens); its rows are the tokens x the kv head's query heads, so one
+// staging of a K or V tile (SPA_T positions, shared by every row) serves G x kv_mul heads.  Each (row,
+// position) score is the sequential dot q . k over the head's elements, then / sqrtf(hs), kept in LDS (rows of
+// SP floats, the launcher's bound on the positions); the row's maximum; expf(s - max) (ref_expf); the sum in
+// position order (one lane per row, all rows of the block in one wave: one wave64 add per position); the
+// division; then out[e] accumulated in position order over the V tiles, a (row, element) pair per thread.
+#define SPA_T 64 // positions per K/V tile
+#define SPA_NS 4 // score chains per thread and tile (rows x SPA_T <= 4 x 256)
+__host__ __device__ inline size_t spa_lds_floats(int rows, int hs, int sp) {
+    return (size_t)rows * hs + (size_t)rows * sp + (size_t)SPA_T * (hs + 4) + 2 * (size_t)rows;
+}
+// One tile of G tokens (from m0) of kv head kvh; NV: value chains per thread (rows x hs <= NV x 256).
+template <int HS, int NV>
+__device__ __forceinline__ void spa_tile(const ProwArgs &a, int G, int SP, int kvh, int m0, float *sm) {
+    const int hs = HS ? HS : a.head_size, kv_mul = a.n_heads / a.n_kv;
+    const int gn = min(G, a.M - m0), R = gn * kv_mul, Rmax = G * kv_mul;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE, HP = hs + 4, hs4 = hs / 4;
+    const int Pmax = a.p0 + m0 + gn; // positions of the tile's last token
+    float *qs = sm, *sc = qs + (size_t)Rmax * hs, *kv = sc + (size_t)Rmax * SP, *rmax = kv + SPA_T * HP,
+          *rsum = rmax + Rmax;
+    const int koff = kvh * hs;
+    auto row_pos = [&](int r) { return a.p0 + m0 + r / kv_mul + 1; };          // P of row r
+    auto row_head = [&](int r) { return kvh * kv_mul + r % kv_mul; };          // query head of row r
+    auto row_tok = [&](int r) { return m0 + r / kv_mul; };                     // token of row r
+    __syncthreads(); // a previous tile's rows are consumed
+    for (int r = wave; r < R; r += 4)
+        for (int c = lane; c < hs4; c += WAVE)
+            ((float4 *)(qs + r * hs))[c] = *(const float4 *)(a.q + (size_t)row_tok(r) * a.dim + (size_t)row_head(r) * hs + 4 * c);
+    // a K or V tile: positions t0 .. t0 + SPA_T - 1 (below Pmax) of the kv head, rows of hs + 4 floats in LDS;
+    // fetch() puts all of a thread's loads (SPA_T x hs / 1024 vectors) in flight at once, put() stores them
+    constexpr int FV = (HS ? HS : 256) * SPA_T / 1024; // vectors per thread (hs <= 256)
+    auto fetch = [&](const float *cache, int t0, float4 (&f)[FV]) {
+#pragma unroll
+        for (int j = 0; j < FV; j++) {
+            const int idx = tid + 256 * j, tt = idx / hs4, c = idx - tt * hs4;
+            f[j] = tt < SPA_T && t0 + tt < Pmax ? *(const float4 *)(cache + (size_t)(t0 + tt) * a.kv_dim + koff + 4 * c)
+                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    auto put = [&](const float4 (&f)[FV]) {
+#pragma unroll
+        for (int j = 0; j < FV; j++) {
+            const int idx = tid + 256 * j, tt = idx / hs4, c = idx - tt * hs4;
+            if (tt < SPA_T) *(float4 *)(kv + tt * HP + 4 * c) = f[j];
+        }
+    };
+    float4 fr[FV];
+    KERNEL_MARK(0);
+    const float rs = sqrtf((float)hs);
+    // (1) scores: thread tid takes position tt = tid % 64 of the tile for rows tid / 64 + 4 j (j < SPA_NS), its
+    // K row read once per 4 elements for all of them; each score the sequential dot over the head's elements
+    const int s_tt = tid % SPA_T, s_r0 = tid / SPA_T;
+    fetch(a.kc, 0, fr);
+    for (int t0 = 0; t0 < Pmax; t0 += SPA_T) {
+        __syncthreads(); // the previous tile is consumed
+        put(fr);
+        __syncthreads();
+        if (t0 + SPA_T < Pmax) fetch(a.kc, t0 + SPA_T, fr); // the next tile in flight during this one
+        float d[SPA_NS];
+#pragma unroll
+        for (int j = 0; j < SPA_NS; j++) d[j] = 0.0f;
+        const float4 *kr = (const float4 *)(kv + s_tt * HP);
+        const float4 *qr[SPA_NS];
+#pragma unroll
+        for (int j = 0; j < SPA_NS; j++) qr[j] = (const float4 *)(qs + min(s_r0 + 4 * j, Rmax - 1) * hs);
+#pragma unroll 4
+        for (int c = 0; c < hs4; c++) {
+            const float4 k4 = kr[c];
+#pragma unroll
+            for (int j = 0; j < SPA_NS; j++) {
+                const float4 q4 = qr[j][c];
+                d[j] += q4.x * k4.x;
+                d[j] += q4.y * k4.y;
+                d[j] += q4.z * k4.z;
+                d[j] += q4.w * k4.w;
+            }
+        }
+        const int t = t0 + s_tt;
+#pragma unroll
+        for (int j = 0; j < SPA_NS; j++) {
+            const int r = s_r0 + 4 * j;
+            if (r < R && t < row_pos(r)) sc[(size_t)r * SP + t] = d[j] / rs;
+        }
+    }
+    __syncthreads();
+    KERNEL_MARK(1);
+    // (2) a wave per row: its maximum, then its exponentials (positions past the row, up to the tile's last
+    // token's, set to 0: the sums below then add +0 there, which leaves a positive sum unchanged)
+    for (int r = wave; r < R; r += 4) {
+        float *row = sc + (size_t)r * SP;
+        const int P = row_pos(r);
+        float mx = -INFINITY;
+        for (int t = lane; t < P; t += WAVE) mx = fmaxf(mx, row[t]);
+        mx = wave_max(mx);
+        for (int t = lane; t < Pmax; t += WAVE) row[t] = t < P ? ref_expf(row[t] - mx) : 0.0f;
+    }
+    __syncthreads();
+    KERNEL_MARK(2);
+    // (3) the sums in position order: lane r of wave 0 adds row r, 8 positions in flight
+    if (wave == 0 && lane < R) {
+        const float *row = sc + (size_t)lane * SP;
+        float s = 0.0f;
+        int t = 0;
+        for (; t + 8 <= Pmax; t += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = row[t + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s = s + v[u];
+        }
+        for (; t < Pmax; t++) s = s + row[t];
+        rsum[lane] = s;
+    }
+    __syncthreads();
+    KERNEL_MARK(3);
+    // the probabilities (0 stays 0 past the row: the value sums add +0 there)
+    for (int r = wave; r < R; r += 4) {
+        float *row = sc + (size_t)r * SP;
+        const float sum = rsum[r];
+        for (int t = lane; t < Pmax; t += WAVE) row[t] = row[t] / sum;
+    }
+    KERNEL_MARK(4);
+    // (4) values: thread tid takes element e = tid % hs of rows tid / hs + (256 / hs) j, the V element read once
+    // per position for all of them; positions in order over the tiles
+    const int v_e = tid % hs, v_r0 = tid / hs, v_rs = 256 / hs;
+    float acc[NV];
+    const float *pr[NV];
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        acc[j] = 0.0f;
+        pr[j] = sc + (size_t)min(v_r0 + v_rs * j, Rmax - 1) * SP;
+    }
+    fetch(a.vc, 0, fr);
+    for (int t0 = 0; t0 < Pmax; t0 += SPA_T) {
+        __syncthreads(); // the probabilities are written, the previous tile consumed
+        put(fr);
+        __syncthreads();
+        if (t0 + SPA_T < Pmax) fetch(a.vc, t0 + SPA_T, fr);
+        const int T = min(SPA_T, Pmax - t0);
+        const float *vt = kv + v_e;
+#pragma unroll 8
+        for (int tt = 0; tt < T; tt++) {
+            const float v = vt[tt * HP];
+#pragma unroll
+            for (int j = 0; j < NV; j++) acc[j] += pr[j][t0 + tt] * v;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        const int r = v_r0 + v_rs * j;
+        if (r < R) a.xb[(size_t)row_tok(r) * a.dim + (size_t)row_head(r) * hs + v_e] = acc[j];
+    }
+    KERNEL_MARK(5);
+}
+
+// Strict prefill attention over tiles of tokens (qwen.c:526-546 for each token and head, in the reference's
+// order): a tile = G consecutive tokens of one kv head; its rows are the tokens x the kv head's query heads, so
+// one staging of a K or V tile (SPA_T positions, shared by every row) serves G x kv_mul heads.  Each (row,
+// position) score is the sequential dot q . k over the head's elements, then / sqrtf(hs), kept in LDS (rows of
+// SP floats, the launcher's bound on the positions); the row's maximum; expf(s - max) (ref_expf); the sum in
+// position order (one lane per row, every row of the tile in one wave: one wave64 add per position); the
+// division; then out[e] accumulated in position order over the V tiles, (row, element) chains per thread.
+// Block y takes tiles y and ntiles - 1 - y (a short and a long causal range: every block the same work).
+template <int HS, int NV>
+__global__ void __launch_bounds__(256) k_p_attn_strict_rows(ProwArgs a, int G, int SP) {
+    extern __shared__ __align__(16) float sm[];
+    const int ntiles = (a.M + G - 1) / G, y = blockIdx.y, y2 = ntiles - 1 - y;
+    spa_tile<HS, NV>(a, G, SP, blockIdx.x, y * G, sm);
+    if (y2 != y) spa_tile<HS, NV>(a, G, SP, blockIdx.x, y2 * G, sm);
+}
+
 // int8 quantization of the rows xb[m] (qwen.c:549, runq.c:571) into the o projection's input
 __global__ void __launch_bounds__(256) k_p_quant_rows(ProwArgs a) {
     extern __shared__ __align__(16) float sv[];
@@ -1233,7 +1405,31 @@ hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
             ((uintptr_t)a.oq & 3) || lds > 65536 || a.n_heads % a.n_kv ||
             (size_t)(a.p0 + a.M + 64) * a.kv_dim * 4 >= 0x7fffffffu)
             return hipErrorInvalidValue;
-        if (hs == 64) hipLaunchKernelGGL(k_p_attn_strict<64>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
+        // tiles of G tokens when their rows' scores fit LDS (G x kv_mul rows, positions up to p0 + M), else a
+        // block per (head, token) that streams the positions
+        const int kvm = a.n_heads / a.n_kv, SP = a.p0 + a.M + 1; // odd row stride: the sums' lanes hit distinct banks
+        int G = 0;
+        for (int g = 4; g >= 1 && !G; g /= 2)
+            if (g * kvm <= 4 * SPA_NS && g * kvm * hs <= 8 * 256 && hs <= 256 && 256 % hs == 0 &&
+                spa_lds_floats(g * kvm, hs, SP) * 4 <= 65536)
+                G = g;
+        if (G) {
+            const int ntiles = (a.M + G - 1) / G;
+            const dim3 grid(a.n_kv, (ntiles + 1) / 2);
+            const size_t sl = spa_lds_floats(G * kvm, hs, SP) * 4;
+            const bool nv4 = G * kvm * hs <= 4 * 256;
+#define SPA_LAUNCH(H)                                                                                          \
+            if (nv4) hipLaunchKernelGGL((k_p_attn_strict_rows<H, 4>), grid, dim3(256), sl, st, a, G, SP);      \
+            else hipLaunchKernelGGL((k_p_attn_strict_rows<H, 8>), grid, dim3(256), sl, st, a, G, SP);
+            if (hs == 64) {
+                SPA_LAUNCH(64)
+            } else if (hs == 128) {
+                SPA_LAUNCH(128)
+            } else {
+                SPA_LAUNCH(0)
+            }
+#undef SPA_LAUNCH
+        } else if (hs == 64) hipLaunchKernelGGL(k_p_attn_strict<64>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
         else if (hs == 128) hipLaunchKernelGGL(k_p_attn_strict<128>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
         else hipLaunchKernelGGL(k_p_attn_strict<0>, dim3(a.n_heads, a.M), dim3(256), lds, st, a);
         hipError_t e = hipGetLastError();
