@@ -101,8 +101,32 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
     return t;
 }
 
+// s + t[16 - r] + ... + t[15] in that order, r in [0, 16): one jump into a run of adds (the last terms of a sum
+// arrive loaded together as the final 16 of the range, instead of one load and add after another).
+__device__ __forceinline__ float seq_add_tail(float s, const float (&t)[16], int r) {
+    switch (r) {
+    case 15: s = s + t[1]; [[fallthrough]];
+    case 14: s = s + t[2]; [[fallthrough]];
+    case 13: s = s + t[3]; [[fallthrough]];
+    case 12: s = s + t[4]; [[fallthrough]];
+    case 11: s = s + t[5]; [[fallthrough]];
+    case 10: s = s + t[6]; [[fallthrough]];
+    case 9: s = s + t[7]; [[fallthrough]];
+    case 8: s = s + t[8]; [[fallthrough]];
+    case 7: s = s + t[9]; [[fallthrough]];
+    case 6: s = s + t[10]; [[fallthrough]];
+    case 5: s = s + t[11]; [[fallthrough]];
+    case 4: s = s + t[12]; [[fallthrough]];
+    case 3: s = s + t[13]; [[fallthrough]];
+    case 2: s = s + t[14]; [[fallthrough]];
+    case 1: s = s + t[15]; [[fallthrough]];
+    default: break;
+    }
+    return s;
+}
+
 // Sum of n floats in index order (one thread; p in LDS, any alignment): the reads of the next 16 values are
-// issued before the current 16 are added (the last batch re-reads itself instead of branching).
+// issued before the current 16 are added, and the last n % 16 are read together and entered by seq_add_tail.
 __device__ __forceinline__ float seq_sum(const float *p, int n) {
     float v = 0.0f;
     int g = 0;
@@ -120,7 +144,12 @@ __device__ __forceinline__ float seq_sum(const float *p, int n) {
             for (int u = 0; u < 16; u++) cur[u] = nxt[u];
         }
     }
-    for (; g < n; g++) v += p[g];
+    if (g < n) {
+        float t[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) t[u] = p[max(n - 16 + u, 0)];
+        v = seq_add_tail(v, t, n - g);
+    }
     return v;
 }
 
