@@ -181,6 +181,11 @@ int mvh_sample_noalloc(const float *logits, int n, int count, float temperature,
  * device (n <= 2^26), and the same restatement compiled for the host CPU (no GPU involved) */
 int mvh_ref_expf(const float *x, int n, float *y);
 int mvh_ref_expf_host(const float *x, int n, float *y);
+/* the strict mode's sequential fp32 sum s = ((0 + x[0]) + x[1]) + ... (rmsnorm's sum of squares and the
+ * softmax sum, qwen.c:339 and qwen.c:349; a row's group products, qwen.c:441-452) by one of its device forms,
+ * n <= 8192: which 0 = the block's speculative segments with `threads` threads (64..1024, a multiple of 64),
+ * 1 = one wave's chain, 2 = one thread's chain (`threads` ignored).  0 on success, -1 on bad arguments. */
+int mvh_seq_sum(const float *x, int n, int which, int threads, float *out);
 /* device state after the last llm_forward/llm_generate step: 0 = residual stream x (dim floats, after the
  * final rmsnorm like qwen.c:569), 1 = key cache of layer `layer` (ctx * kv_dim), 2 = value cache */
 int llm_read_state(llm_model *m, int which, int layer, float *dst, size_t count);

@@ -90,6 +90,7 @@ def lib():
     L.mvh_ref_expf.argtypes = [vp, i32, vp]
     L.mvh_read_floor.argtypes = [C.c_size_t, i32, i32, i32, i32, C.POINTER(C.c_float)]
     L.mvh_ref_expf_host.argtypes = [vp, i32, vp]
+    L.mvh_seq_sum.argtypes = [vp, i32, i32, i32, vp]
     L.llm_set_strict.argtypes = [vp, i32]
     L.llm_get_strict.argtypes = [vp]
     _lib = L
@@ -160,6 +161,17 @@ def read_floor(nbytes, copies, blocks, nt=True, reps=20):
     if lib().mvh_read_floor(nbytes, copies, blocks, int(nt), reps, C.byref(us)) != 0:
         raise RuntimeError("mvh_read_floor failed")
     return us.value
+
+
+def seq_sum(x, which="block", threads=512):
+    """the strict mode's sequential fp32 sum ((0 + x[0]) + x[1]) + ... on the device: which "block" (the block's
+    speculative segments, `threads` threads), "wave" (one wave's chain) or "thread" (one thread's chain)"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(1, np.float32)
+    w = {"block": 0, "wave": 1, "thread": 2}[which]
+    if lib().mvh_seq_sum(_ptr(x), x.size, w, threads, _ptr(out)) != 0:
+        raise RuntimeError("mvh_seq_sum failed")
+    return out[0]
 
 
 def ref_expf(x, host=False):

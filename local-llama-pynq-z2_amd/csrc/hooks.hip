@@ -7,6 +7,7 @@
 #include "host_common.h"
 #include "prefill.h"
 #include "ref_expf.h"
+#include "seqsum.h"
 
 namespace {
 int hook_device(const char *who) {
@@ -256,6 +257,50 @@ extern "C" int mvh_ref_expf(const float *x, int n, float *y) {
     if (rc) fprintf(stderr, "mvh_ref_expf: HIP error %s\n", hipGetErrorString(hipGetLastError()));
     hipFree(dx);
     hipFree(dy);
+    return rc;
+}
+
+// The strict mode's sequential sums on their own: block_seq_sum (the RMSNorm sum of squares, the long softmax
+// sums), wave_seq_sum (the short softmax sums) and seq_sum (a GEMV row's group products, one thread).
+template <int WHICH>
+__global__ void __launch_bounds__(1024) k_seq_sum(const float *x, int n, float *out) {
+    extern __shared__ __align__(16) float s_terms[];
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s_terms[i] = x[i];
+    __syncthreads();
+    float s = 0.0f;
+    if constexpr (WHICH == 0) {
+        s = block_seq_sum(s_terms, n, (uint8_t *)(s_terms + ((n + 3) & ~3)));
+    } else if constexpr (WHICH == 1) {
+        if (threadIdx.x < WAVE) s = wave_seq_sum(s_terms, n);
+    } else {
+        if (threadIdx.x == 0) s = seq_sum(s_terms, n);
+    }
+    if (threadIdx.x == 0) out[0] = s;
+}
+
+extern "C" int mvh_seq_sum(const float *x, int n, int which, int threads, float *out) {
+    if (!x || !out || n < 1 || n > 8192 || which < 0 || which > 2 ||
+        (which == 0 && (threads < WAVE || threads > SEQ_MAX_WAVES * WAVE || threads % WAVE))) {
+        fprintf(stderr, "mvh_seq_sum: bad arguments (n=%d which=%d threads=%d)\n", n, which, threads);
+        return -1;
+    }
+    if (hook_device("mvh_seq_sum")) return -1;
+    const int nt = which == 0 ? threads : WAVE;
+    const size_t lds = (size_t)((n + 3) & ~3) * 4 + seq_sum_scratch_bytes(nt);
+    float *dx = nullptr, *dout = nullptr;
+    int rc = -1;
+    if (hipMalloc(&dx, (size_t)n * 4) == hipSuccess && hipMalloc(&dout, 4) == hipSuccess &&
+        hipMemcpy(dx, x, (size_t)n * 4, hipMemcpyHostToDevice) == hipSuccess) {
+        if (which == 0) hipLaunchKernelGGL(k_seq_sum<0>, dim3(1), dim3(nt), lds, 0, dx, n, dout);
+        else if (which == 1) hipLaunchKernelGGL(k_seq_sum<1>, dim3(1), dim3(nt), lds, 0, dx, n, dout);
+        else hipLaunchKernelGGL(k_seq_sum<2>, dim3(1), dim3(nt), lds, 0, dx, n, dout);
+        if (hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+            hipMemcpy(out, dout, 4, hipMemcpyDeviceToHost) == hipSuccess)
+            rc = 0;
+    }
+    if (rc) fprintf(stderr, "mvh_seq_sum: HIP error %s\n", hipGetErrorString(hipGetLastError()));
+    hipFree(dx);
+    hipFree(dout);
     return rc;
 }
 
