@@ -1220,33 +1220,49 @@ __device__ __forceinline__ void spa_tile(const ProwArgs &a, int G, int SP, int k
     // a K or V tile: positions t0 .. t0 + SPA_T - 1 (below Pmax) of the kv head, rows of hs + 4 floats in LDS;
     // fetch() puts all of a thread's loads (SPA_T x hs / 1024 vectors) in flight at once, put() stores them
     constexpr int FV = (HS ? HS : 256) * SPA_T / 1024; // vectors per thread (hs <= 256)
-    auto fetch = [&](const float *cache, int t0, float4 (&f)[FV]) {
+    // (buffer loads: a position past the range reads zeros through an out-of-range offset, so every load is issued
+    // unconditionally and each staging waits for its own tile's loads only)
+    const int nrec = (int)(((size_t)(Pmax - 1) * a.kv_dim + hs) * 4);
+    const auto rs_k = __builtin_amdgcn_make_buffer_rsrc((void *)(a.kc + koff), 0, nrec, 0x00020000);
+    const auto rs_v = __builtin_amdgcn_make_buffer_rsrc((void *)(a.vc + koff), 0, nrec, 0x00020000);
+    auto fetch = [&](__amdgpu_buffer_rsrc_t rs, int t0, float4 (&f)[FV]) {
 #pragma unroll
         for (int j = 0; j < FV; j++) {
             const int idx = tid + 256 * j, tt = idx / hs4, c = idx - tt * hs4;
-            f[j] = tt < SPA_T && t0 + tt < Pmax ? *(const float4 *)(cache + (size_t)(t0 + tt) * a.kv_dim + koff + 4 * c)
-                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const bool ok = tt < SPA_T && t0 + tt < Pmax;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(
+                rs, ok ? (uint32_t)((t0 + tt) * a.kv_dim + 4 * c) * 4u : 0x80000000u, 0, 0);
+            f[j] = *(const float4 *)&v;
         }
     };
     auto put = [&](const float4 (&f)[FV]) {
 #pragma unroll
         for (int j = 0; j < FV; j++) {
             const int idx = tid + 256 * j, tt = idx / hs4, c = idx - tt * hs4;
-            if (tt < SPA_T) *(float4 *)(kv + tt * HP + 4 * c) = f[j];
+            if (HS || tt < SPA_T) *(float4 *)(kv + tt * HP + 4 * c) = f[j]; // (a fixed head size fills FV exactly)
         }
     };
-    float4 fr[FV];
+    // DK tiles in flight: a tile's compute is shorter than a round trip to the cache, so the loads of the tiles
+    // DK ahead leave as each tile is staged (register sets used in turn, the tile loop unrolled by DK)
+    constexpr int DK = (HS && HS <= 64) ? 4 : 2;
+    float4 fr[DK][FV];
+    const int nkt = (Pmax + SPA_T - 1) / SPA_T;
     KERNEL_MARK(0);
     const float rs = sqrtf((float)hs);
     // (1) scores: thread tid takes position tt = tid % 64 of the tile for rows tid / 64 + 4 j (j < SPA_NS), its
     // K row read once per 4 elements for all of them; each score the sequential dot over the head's elements
     const int s_tt = tid % SPA_T, s_r0 = tid / SPA_T;
-    fetch(a.kc, 0, fr);
-    for (int t0 = 0; t0 < Pmax; t0 += SPA_T) {
+#pragma unroll
+    for (int dd = 0; dd < DK; dd++) fetch(rs_k, dd * SPA_T, fr[dd]); // (tiles past the range: zeros, no traffic)
+    for (int k0 = 0; k0 < nkt; k0 += DK)
+#pragma unroll
+    for (int dd = 0; dd < DK; dd++) {
+        const int kt = k0 + dd, t0 = kt * SPA_T;
+        if (kt >= nkt) break;
         __syncthreads(); // the previous tile is consumed
-        put(fr);
+        put(fr[dd]);
         __syncthreads();
-        if (t0 + SPA_T < Pmax) fetch(a.kc, t0 + SPA_T, fr); // the next tile in flight during this one
+        fetch(rs_k, (kt + DK) * SPA_T, fr[dd]);
         float d[SPA_NS];
 #pragma unroll
         for (int j = 0; j < SPA_NS; j++) d[j] = 0.0f;
@@ -1290,14 +1306,19 @@ __device__ __forceinline__ void spa_tile(const ProwArgs &a, int G, int SP, int k
     // (3) the sums in position order: lane r of wave 0 adds row r, 8 positions in flight
     if (wave == 0 && lane < R) {
         const float *row = sc + (size_t)lane * SP;
+        const float4 *row4 = (const float4 *)row;
         float s = 0.0f;
         int t = 0;
         for (; t + 8 <= Pmax; t += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = row[t + u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) s = s + v[u];
+            const float4 v0 = row4[t / 4], v1 = row4[t / 4 + 1];
+            s = s + v0.x;
+            s = s + v0.y;
+            s = s + v0.z;
+            s = s + v0.w;
+            s = s + v1.x;
+            s = s + v1.y;
+            s = s + v1.z;
+            s = s + v1.w;
         }
         for (; t < Pmax; t++) s = s + row[t];
         rsum[lane] = s;
@@ -1321,16 +1342,51 @@ __device__ __forceinline__ void spa_tile(const ProwArgs &a, int G, int SP, int k
         acc[j] = 0.0f;
         pr[j] = sc + (size_t)min(v_r0 + v_rs * j, Rmax - 1) * SP;
     }
-    fetch(a.vc, 0, fr);
-    for (int t0 = 0; t0 < Pmax; t0 += SPA_T) {
+#pragma unroll
+    for (int dd = 0; dd < DK; dd++) fetch(rs_v, dd * SPA_T, fr[dd]);
+    for (int k0 = 0; k0 < nkt; k0 += DK)
+#pragma unroll
+    for (int dd = 0; dd < DK; dd++) {
+        const int kt = k0 + dd, t0 = kt * SPA_T;
+        if (kt >= nkt) break;
         __syncthreads(); // the probabilities are written, the previous tile consumed
-        put(fr);
+        put(fr[dd]);
         __syncthreads();
-        if (t0 + SPA_T < Pmax) fetch(a.vc, t0 + SPA_T, fr);
+        fetch(rs_v, (kt + DK) * SPA_T, fr[dd]);
         const int T = min(SPA_T, Pmax - t0);
         const float *vt = kv + v_e;
-#pragma unroll 8
-        for (int tt = 0; tt < T; tt++) {
+        int tt = 0;
+        // 4 positions a step: each row's 4 weights in one load (rows and t0 are 16-byte aligned), then the
+        // products and adds position by position; a full tile as straight-line code (the loads of later steps
+        // scheduled ahead of earlier steps' arithmetic)
+        auto step4 = [&](int s) {
+            const float v0 = vt[s * HP], v1 = vt[(s + 1) * HP], v2 = vt[(s + 2) * HP], v3 = vt[(s + 3) * HP];
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const float4 w = *(const float4 *)(pr[j] + t0 + s);
+                acc[j] += w.x * v0;
+                acc[j] += w.y * v1;
+                acc[j] += w.z * v2;
+                acc[j] += w.w * v3;
+            }
+        };
+        if (T == SPA_T) {
+#pragma unroll
+            for (int s = 0; s < SPA_T; s += 4) step4(s);
+            tt = SPA_T;
+        }
+        for (; tt + 4 <= T; tt += 4) {
+            const float v0 = vt[tt * HP], v1 = vt[(tt + 1) * HP], v2 = vt[(tt + 2) * HP], v3 = vt[(tt + 3) * HP];
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const float4 w = *(const float4 *)(pr[j] + t0 + tt);
+                acc[j] += w.x * v0;
+                acc[j] += w.y * v1;
+                acc[j] += w.z * v2;
+                acc[j] += w.w * v3;
+            }
+        }
+        for (; tt < T; tt++) {
             const float v = vt[tt * HP];
 #pragma unroll
             for (int j = 0; j < NV; j++) acc[j] += pr[j][t0 + tt] * v;
@@ -1407,7 +1463,9 @@ hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
             return hipErrorInvalidValue;
         // tiles of G tokens when their rows' scores fit LDS (G x kv_mul rows, positions up to p0 + M), else a
         // block per (head, token) that streams the positions
-        const int kvm = a.n_heads / a.n_kv, SP = a.p0 + a.M + 1; // odd row stride: the sums' lanes hit distinct banks
+        // score rows of SP = 4 x odd floats: 16-byte aligned (the value chains read 4 weights a load) and the sums'
+        // lanes, one per row, on distinct banks
+        const int kvm = a.n_heads / a.n_kv, SP = 4 * (((a.p0 + a.M + 3) / 4) | 1);
         int G = 0;
         for (int g = 4; g >= 1 && !G; g /= 2)
             if (g * kvm <= 4 * SPA_NS && g * kvm * hs <= 8 * 256 && hs <= 256 && 256 % hs == 0 &&
