@@ -96,9 +96,11 @@ GemvShape gemv_pick_shape(const TiledMat &T, int pro, int epi, int ordered, int 
         s.grid = iters;
         // Ordered sums: one row-block per block, so that a small matrix is spread over as many CUs as it has
         // row-blocks (a CU pulls its block's bytes at a few tens of GB/s; the llama2.c 768/12L shapes: 12 ->
-        // 96 blocks for o and down, 2834 -> 3169 tok/s with 8-row blocks).  The SwiGLU epilogue's row-blocks
-        // per block are fixed by the quantization group.
-        if (s.ord && epi != EPI_SWIGLU) {
+        // 96 blocks for o and down, 2834 -> 3169 tok/s with 8-row blocks).  Not where that would put more
+        // blocks than CUs: the Qwen2-7B shape's strict QKV GEMV keeps 144 blocks of two row-blocks instead of
+        // 288 of one (13.6 -> 11.6 us; the CUs holding two blocks ran two sequential RMSNorm sums).  The
+        // SwiGLU epilogue's row-blocks per block are fixed by the quantization group.
+        if (s.ord && epi != EPI_SWIGLU && T.nblocks <= cus) {
             s.nb = 1;
             s.grid = T.nblocks;
         }

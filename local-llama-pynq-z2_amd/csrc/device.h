@@ -126,7 +126,8 @@ __device__ __forceinline__ float seq_add_tail(float s, const float (&t)[16], int
 }
 
 // Sum of n floats in index order (one thread; p in LDS, any alignment): the reads of the next 16 values are
-// issued before the current 16 are added, and the last n % 16 are read together and entered by seq_add_tail.
+// issued before the current 16 are added, and the last n % 16 are read together and entered by seq_add_tail
+// (sums of fewer than 16 values: one read and add after another).
 __device__ __forceinline__ float seq_sum(const float *p, int n) {
     float v = 0.0f;
     int g = 0;
@@ -144,11 +145,16 @@ __device__ __forceinline__ float seq_sum(const float *p, int n) {
             for (int u = 0; u < 16; u++) cur[u] = nxt[u];
         }
     }
-    if (g < n) {
+    if (g < n && n >= 16) {
+        // the final 16 values from one base address (immediate offsets: no per-value address registers kept
+        // live across a caller's loop)
+        const float *b = p + (n - 16);
         float t[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) t[u] = p[max(n - 16 + u, 0)];
+        for (int u = 0; u < 16; u++) t[u] = b[u];
         v = seq_add_tail(v, t, n - g);
+    } else {
+        for (; g < n; g++) v += p[g];
     }
     return v;
 }

@@ -29,7 +29,8 @@
 
 
 // s + a[i] + ... + a[i1 - 1] in order (a: LDS, the same addresses in every lane): batches of 16 as broadcast
-// reads, then the remaining < 16 terms through seq_add_tail.  a is 16-byte aligned and i a multiple of 4.
+// reads, then the remaining < 16 terms through seq_add_tail (a sum of fewer than 16 terms: one read and add
+// after another).  a is 16-byte aligned and i a multiple of 4.
 __device__ __forceinline__ float seq_chain(float s, const float *a, int i, int i1) {
     const float4 *a4 = (const float4 *)a;
     if (i + 16 <= i1) {
@@ -51,11 +52,14 @@ __device__ __forceinline__ float seq_chain(float s, const float *a, int i, int i
             for (int r = 0; r < 4; r++) cur[r] = nxt[r];
         }
     }
-    if (i < i1) {
+    if (i < i1 && i1 >= 16) {
+        const float *b = a + (i1 - 16); // one base address, immediate offsets
         float t[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) t[u] = a[max(i1 - 16 + u, 0)];
+        for (int u = 0; u < 16; u++) t[u] = b[u];
         s = seq_add_tail(s, t, i1 - i);
+    } else {
+        for (; i < i1; i++) s = s + a[i];
     }
     return s;
 }
