@@ -305,6 +305,30 @@ def traffic_from(pmc_dir, kind):
     return res
 
 
+def code_sizes():
+    """{kind: {kernel: bytes of machine code}} of the decode kernels in the built library, read from its gfx950
+    code object with the ROCm LLVM tools.  FETCH_SIZE counts a launch's instruction fetches too: every kernel
+    starts with invalidated L2 caches, so each of the 8 XCDs fetches the code its waves execute, up to 8 x these
+    bytes per launch."""
+    import subprocess
+    import tempfile
+    llvm = "/opt/rocm/llvm/bin"
+    lib = os.path.join(PKG, "libmatvec_hip.so")
+    with tempfile.TemporaryDirectory() as td:
+        fat, co = os.path.join(td, "fatbin"), os.path.join(td, "gfx950.co")
+        subprocess.run(["objcopy", "--dump-section", f".hip_fatbin={fat}", lib], check=True)
+        subprocess.run([f"{llvm}/clang-offload-bundler", "--unbundle", "--type=o", f"--input={fat}",
+                        "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True)
+        syms = subprocess.run([f"{llvm}/llvm-readelf", "-s", "--wide", "--demangle", co], check=True,
+                              capture_output=True, text=True).stdout
+    sizes = {}
+    for line in syms.splitlines():
+        f = line.split(None, 7)
+        if len(f) == 8 and f[3] == "FUNC":
+            sizes[f[7]] = int(f[2])
+    return {kind: {k: v for k, v in sorted(sizes.items()) if sym in k} for kind, sym in KERNEL_SYMBOL.items()}
+
+
 def trace_summary(csv_path):
     """a rocprofv3 --kernel-trace CSV grouped by (kernel, grid, workgroup): share of GPU time, calls, avg / median /
     min / max microseconds (the prefill GEMM shapes share one kernel name and differ by grid)"""
@@ -609,11 +633,18 @@ def main():
                     help="with --traffic-from: print every kernel kind's HBM bytes per launch and stop")
     ap.add_argument("--floor", action="store_true",
                     help="the plain-read floor of each layer GEMV's bytes per launch (C3 and C5 shapes), and stop")
+    ap.add_argument("--code-sizes", action="store_true",
+                    help="print the machine-code bytes of each decode kernel kind in the built library, and stop")
     ap.add_argument("--trace-summary", default=None, metavar="CSV",
                     help="print a rocprofv3 kernel trace grouped by kernel and grid, and stop")
     a = ap.parse_args()
     if a.trace_summary:
         return trace_summary(a.trace_summary)
+    if a.code_sizes:
+        for kind, ks in code_sizes().items():
+            for k, b in ks.items():
+                print(f"{kind:12s} {b / 1e3:6.1f} KB of code, x 8 XCDs {8 * b / 1e6:6.3f} MB  {k}")
+        return
     if a.traffic_from and a.traffic_all:
         for kind in KERNEL_SYMBOL:
             r = traffic_from(a.traffic_from, kind)
