@@ -126,11 +126,24 @@ __device__ __forceinline__ float seq_add_tail(float s, const float (&t)[16], int
 }
 
 // Sum of n floats in index order (one thread; p in LDS, any alignment): the reads of the next 16 values are
-// issued before the current 16 are added, and the last n % 16 are read together and entered by seq_add_tail
-// (sums of fewer than 16 values: one read and add after another).
+// issued before the current 16 are added, and the last n % 16 are read together and entered by seq_add_tail;
+// 17 to 31 values are read in one round, both batches at once (sums of fewer than 16 values: one read and add
+// after another).
 __device__ __forceinline__ float seq_sum(const float *p, int n) {
     float v = 0.0f;
     int g = 0;
+    if (n > 16 && n < 32) { // both batches read at once: the first 16 values and the last 16
+        const float *b = p + (n - 16);
+        float t0[16], t[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            t0[u] = p[u];
+            t[u] = b[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) v += t0[u];
+        return seq_add_tail(v, t, n - 16);
+    }
     if (n >= 16) {
         float cur[16], nxt[16];
 #pragma unroll

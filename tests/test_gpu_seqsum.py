@@ -30,8 +30,8 @@ def same(x, y):
 def cases():
     rng = np.random.default_rng(20)
     out = []
-    lengths = [1, 2, 3, 15, 16, 17, 31, 63, 64, 65, 127, 255, 256, 257, 288, 511, 513, 767, 768, 769, 896, 1000,
-               2047, 3584, 4096, 4864, 8192]
+    lengths = [1, 2, 3, 15, 16, 17, 28, 31, 32, 33, 47, 48, 49, 63, 64, 65, 112, 127, 152, 255, 256, 257, 288, 511,
+               513, 592, 767, 768, 769, 896, 1000, 2047, 3584, 4096, 4864, 8192]
     for n in lengths:
         x = rng.standard_normal(n).astype(np.float32)
         out.append((f"squares n={n}", x * x))
