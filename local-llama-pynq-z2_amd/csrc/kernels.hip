@@ -691,10 +691,12 @@ template <int WB, int GSZ, int SF32, int PRO, int EPI>
 static hipError_t launch_one(const GemvArgs &a, int grid, hipStream_t st) {
     const int threads = a.kw * a.nb * WAVE;
     const size_t lds = gemv_lds_bytes(a, PRO, EPI, threads);
-    if (a.depth == 1) {
+    // the QKV epilogue keeps one weight batch in flight per wave: with two, its 1024-thread kernels would not fit
+    // their registers
+    if (a.depth == 1 || EPI == EPI_QKV) {
         if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 1, 1>), dim3(grid), dim3(threads), lds, st, a);
         else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 1, 0>), dim3(grid), dim3(threads), lds, st, a);
-    } else {
+    } else if constexpr (EPI != EPI_QKV) {
         if (a.nt) hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 1>), dim3(grid), dim3(threads), lds, st, a);
         else hipLaunchKernelGGL((k_gemv<WB, GSZ, SF32, PRO, EPI, 2, 0>), dim3(grid), dim3(threads), lds, st, a);
     }

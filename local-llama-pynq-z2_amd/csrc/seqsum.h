@@ -28,11 +28,26 @@
 #define SEQ_MAX_WAVES 16 // segments (waves) a block may use
 
 
-// s + a[i] + ... + a[i1 - 1] in order (a: LDS, the same addresses in every lane): batches of 16 as broadcast
-// reads, then the remaining < 16 terms through seq_add_tail (a sum of fewer than 16 terms: one read and add
-// after another).  a is 16-byte aligned and i a multiple of 4.
+// s + a[i] + ... + a[i1 - 1] in order (a: LDS, the same addresses in every lane): blocks of 32 terms read at
+// once, then batches of 16 as broadcast reads, then the remaining < 16 terms through seq_add_tail (a sum of fewer
+// than 16 terms: one read and add after another).  a is 16-byte aligned and i a multiple of 4.  (The blocks of
+// 32: a 448-term chain 6.0k -> 4.6k cycles, 112 terms 1.7k -> 1.5k, measured alone on 512 threads.)
 __device__ __forceinline__ float seq_chain(float s, const float *a, int i, int i1) {
     const float4 *a4 = (const float4 *)a;
+    // whole blocks of 32 terms: the block's eight 16-byte reads issued together, then its 32 adds
+    while (i + 32 <= i1) {
+        float4 t4[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) t4[r] = a4[i / 4 + r];
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            s = s + t4[r].x;
+            s = s + t4[r].y;
+            s = s + t4[r].z;
+            s = s + t4[r].w;
+        }
+        i += 32;
+    }
     if (i + 16 <= i1) {
         float4 cur[4], nxt[4];
 #pragma unroll
