@@ -1,10 +1,11 @@
-"""bench.py's host-side reporting, on the CPU: the single-GPU refusal, the rocprofv3 kernel-trace summary and the
+"""bench.py's host-side reporting, on the CPU: the single-GPU refusal, the rocprofv3 kernel-trace summary, the
 HBM traffic per launch from the two counter passes (each counter scaled by what it reads for the calibration
-pass over 1 GiB).  The CSVs are written here in rocprofv3's column layout; the figures are set by hand so that
+pass over 1 GiB) and the decode kernels' code sizes in the built library.  The CSVs are written here in rocprofv3's column layout; the figures are set by hand so that
 every expected number follows from the arithmetic in the docstrings."""
 import csv
 import importlib.util
 import os
+import shutil
 import subprocess
 import sys
 
@@ -83,3 +84,20 @@ def test_trace_summary_groups_by_kernel_and_grid(bench, tmp_path, capsys):
     assert second[0] == "40.00%" and second[2] == "1" and second[4] == "4.00" and second[12] == "200"
     third = lines[2].split()
     assert third[0] == "20.00%" and lines[2].endswith(HEAD)
+
+
+def test_code_sizes_cover_every_decode_kernel_kind(bench):
+    """`bench.py --code-sizes` reads the built library's gfx950 code object: every decode kernel kind has code of a
+    plausible size (a few to a few tens of KB), and the kinds' instantiations carry their template arguments"""
+    lib = os.path.join(ROOT, "local-llama-pynq-z2_amd", "libmatvec_hip.so")
+    tools = [shutil.which("objcopy"), "/opt/rocm/llvm/bin/clang-offload-bundler", "/opt/rocm/llvm/bin/llvm-readelf"]
+    if not os.path.exists(lib) or not all(t and os.path.exists(t) for t in tools):
+        pytest.skip("needs the built library and the ROCm LLVM tools")
+    sizes = bench.code_sizes()
+    assert set(sizes) == set(bench.KERNEL_SYMBOL)
+    for kind, ks in sizes.items():
+        assert ks, kind
+        for name, b in ks.items():
+            assert bench.KERNEL_SYMBOL[kind] in name
+            assert 1000 < b < 100000, (name, b)
+    assert GATEUP in sizes["gateup_gemv"]
