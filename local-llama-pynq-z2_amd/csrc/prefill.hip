@@ -1407,13 +1407,13 @@ __device__ __forceinline__ void spa_tile(const ProwArgs &a, int G, int SP, int k
 // SP floats, the launcher's bound on the positions); the row's maximum; expf(s - max) (ref_expf); the sum in
 // position order (one lane per row, every row of the tile in one wave: one wave64 add per position); the
 // division; then out[e] accumulated in position order over the V tiles, (row, element) chains per thread.
-// Block y takes tiles y and ntiles - 1 - y (a short and a long causal range: every block the same work).
+// One tile per block, the longest causal ranges first (two blocks per CU at 512 tokens; pairing a short and a
+// long range in one block, every block the same work, measured 6% slower: fewer waves in flight per CU).
 template <int HS, int NV>
 __global__ void __launch_bounds__(256) k_p_attn_strict_rows(ProwArgs a, int G, int SP) {
     extern __shared__ __align__(16) float sm[];
-    const int ntiles = (a.M + G - 1) / G, y = blockIdx.y, y2 = ntiles - 1 - y;
+    const int ntiles = (a.M + G - 1) / G, y = ntiles - 1 - (int)blockIdx.y;
     spa_tile<HS, NV>(a, G, SP, blockIdx.x, y * G, sm);
-    if (y2 != y) spa_tile<HS, NV>(a, G, SP, blockIdx.x, y2 * G, sm);
 }
 
 // int8 quantization of the rows xb[m] (qwen.c:549, runq.c:571) into the o projection's input
@@ -1473,7 +1473,7 @@ hipError_t launch_p_attention(const ProwArgs &a, hipStream_t st) {
                 G = g;
         if (G) {
             const int ntiles = (a.M + G - 1) / G;
-            const dim3 grid(a.n_kv, (ntiles + 1) / 2);
+            const dim3 grid(a.n_kv, ntiles);
             const size_t sl = spa_lds_floats(G * kvm, hs, SP) * 4;
             const bool nv4 = G * kvm * hs <= 4 * 256;
 #define SPA_LAUNCH(H)                                                                                          \
